@@ -1,0 +1,193 @@
+"""Throughput benchmark of the INT8 vision path on one MI355X.
+
+Workload (default): the MobileNetV4-Conv-Small-shaped int8 classifier,
+224x224x3, batch 256 per step, random-init seeded weights, synthetic uniform
+int8 images resident in HBM before timing starts. One step = one forward pass
+of the batch through every op of the plan (ug_enqueue_device).
+
+Prints ONE JSON line. Besides the headline images/s it reports:
+  roofline      the op with the largest average launch time, its algorithmic
+                bytes (or ops) per launch over its HIP-event duration
+  cpu_baseline  the reference's portable C runtime (oracle/_ref, built from
+                the reference sources) on this host's cores, batch-1 plans
+  secondary     int8 conv TOPS (1x1 head GEMM, 3x3 implicit GEMM, batch 512)
+                and depthwise HBM GB/s (four cases, batch 64)
+"""
+import argparse
+import ctypes as C
+import json
+import multiprocessing as mp
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "unoq-dsp_amd"))
+
+import uq_plan as P  # noqa: E402
+import uq_workloads as W  # noqa: E402
+from uq_native import DeviceBuffer, Graph, open_library  # noqa: E402
+
+METRIC = "images/sec @ batch 256, MobileNetV4-S int8 224²; conv int8 TOPS + DW HBM GB/s"
+HBM_PEAK = 8.0e12          # bytes/s
+INT8_PEAK = 5.0e15         # dense int8 MFMA ops/s
+RIDGE = INT8_PEAK / HBM_PEAK
+REF_RELEASE = ROOT / "oracle" / "_ref" / "libuq_ref_release.so"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_device(lib, graph, images, steps, warmup, seed=7):
+    x = P.random_input(graph.plan, images, seed)
+    din = DeviceBuffer(lib, x.nbytes)
+    dout = DeviceBuffer(lib, images * graph.output_bytes)
+    din.upload(x)
+    for _ in range(warmup):
+        rc = lib.ug_run_device(din.ptr, dout.ptr, images)
+        assert rc == 0, rc
+    assert lib.ug_synchronize() == 0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        rc = lib.ug_enqueue_device(din.ptr, dout.ptr, images)
+        assert rc == 0, rc
+    assert lib.ug_synchronize() == 0
+    seconds = time.perf_counter() - t0
+    # Per-op HIP-event durations over the same number of steps.
+    graph.profile(1)
+    for _ in range(steps):
+        rc = lib.ug_run_device(din.ptr, dout.ptr, images)
+        assert rc == 0, rc
+    counters = graph.profile(2)
+    graph.profile(0)
+    din.free()
+    dout.free()
+    runs = max(int(counters[0]), 1)
+    per_op_ns = counters[2:2 + lib.ug_op_count()].astype(np.float64) / runs
+    return seconds, per_op_ns
+
+
+def _cpu_worker(args):
+    plan, seconds, seed = args
+    lib = C.CDLL(str(REF_RELEASE))
+    lib.ug_load.argtypes = [C.c_void_p, C.c_uint32]
+    lib.ug_run.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32]
+    buf = C.create_string_buffer(plan, len(plan))
+    assert lib.ug_load(buf, len(plan)) == 0
+    ib, ob = P.input_bytes(plan), P.output_bytes(plan)
+    x = P.random_input(plan, 1, seed)
+    y = np.empty(ob, np.int8)
+    lib.ug_run(x.ctypes.data, ib, y.ctypes.data, ob)  # warm-up
+    done, t0 = 0, time.perf_counter()
+    while True:
+        assert lib.ug_run(x.ctypes.data, ib, y.ctypes.data, ob) == 0
+        done += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    return done, time.perf_counter() - t0
+
+
+def cpu_baseline(plan, seconds_per_worker=1.5):
+    if not REF_RELEASE.exists():
+        return None
+    workers = max(1, min(16, len(os.sched_getaffinity(0))))
+    ctx = mp.get_context("spawn")
+    with ctx.Pool(workers) as pool:
+        res = pool.map(_cpu_worker, [(plan, seconds_per_worker, 100 + i) for i in range(workers)])
+    rate = sum(d / t for d, t in res)
+    images = sum(d for d, _ in res)
+    return {"value": round(rate, 2), "unit": "images/s", "cores": workers, "kind": "reference",
+            "sample": f"{images} MobileNetV4-S batch-1 images via ug_run, {workers} processes x ~{seconds_per_worker}s "
+                      f"(reference runtime/graph.c+qnn.c+gemm.c, release macros, gcc -O3)"}
+
+
+def roofline_entry(costs, per_op_ns):
+    i = int(np.argmax(per_op_ns))
+    c = costs[i]
+    dur = per_op_ns[i] * 1e-9
+    ai = c["ops"] / c["bytes"] if c["bytes"] else 0.0
+    if c["ops"] and ai >= RIDGE:
+        achieved, peak, unit, bound = c["ops"] / dur / 1e12, INT8_PEAK / 1e12, "TOP/s", "mfma"
+    else:
+        achieved, peak, unit, bound = c["bytes"] / dur / 1e9, HBM_PEAK / 1e9, "GB/s", "hbm"
+    return i, {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+               "frac": round(achieved / peak, 4), "traffic": None, "op": i, "code": c["code"],
+               "algorithmic_bytes": c["bytes"], "algorithmic_ops": c["ops"], "avg_ns": round(float(per_op_ns[i]), 1)}
+
+
+def secondary(lib, steps):
+    out = {}
+    for name in ("head", "conv3x3"):
+        plan, images = W.WORKLOADS[name]()
+        g = Graph(plan, lib)
+        sec, per_op = time_device(lib, g, images, steps, 2)
+        ops = sum(c["ops"] for c in P.op_costs(plan, images))
+        out[name] = {"images": images, "ms": round(sec / steps * 1e3, 4), "tops": round(ops / (sec / steps) / 1e12, 2),
+                     "kernel_tops": round(ops / (per_op.sum() * 1e-9) / 1e12, 2)}
+    for name in ("dw3s1", "dw3s2", "dw5s1", "dw5s2"):
+        plan, images = W.WORKLOADS[name]()
+        g = Graph(plan, lib)
+        sec, per_op = time_device(lib, g, images, steps, 2)
+        nbytes = sum(c["bytes"] for c in P.op_costs(plan, images))
+        out[name] = {"images": images, "ms": round(sec / steps * 1e3, 4),
+                     "gbps": round(nbytes / (sec / steps) / 1e9, 1),
+                     "kernel_gbps": round(nbytes / (per_op.sum() * 1e-9) / 1e9, 1)}
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="mnv4")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--per-op", action="store_true", help="print the per-op table to stderr")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); images are independent, so N GPUs "
+              f"would each run this same per-GPU batch", file=sys.stderr)
+        sys.exit(2)
+    plan, images = W.WORKLOADS[args.workload]()
+    # The CPU baseline runs first, in child processes, before this process
+    # touches the GPU.
+    cpu = None if args.no_cpu else cpu_baseline(W.WORKLOADS[args.workload](images=1)[0])
+    lib = open_library()
+    graph = Graph(plan, lib)
+    seconds, per_op_ns = time_device(lib, graph, images, args.steps, args.warmup)
+    costs = P.op_costs(plan, images)
+    if args.per_op:
+        for i, (c, ns) in enumerate(zip(costs, per_op_ns)):
+            log(f"op {i:3d} code {c['code']:2d} {ns / 1e3:9.2f} us  {c['bytes'] / ns:8.1f} GB/s  "
+                f"{(c['ops'] / ns / 1e3 if c['ops'] else 0):8.1f} TOP/s")
+        log(f"sum of op times {per_op_ns.sum() / 1e3:.1f} us, wall per step {seconds / args.steps * 1e6:.1f} us")
+    _, roof = roofline_entry(costs, per_op_ns)
+    ms = seconds / args.steps * 1e3
+    result = {
+        "metric": METRIC, "value": round(images * args.steps / seconds, 1), "unit": "images/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded uniform int8 images, random-init int8 weights)",
+        "config": {"workload": f"{args.workload}: MobileNetV4-Conv-Small-shaped int8 classifier 224x224x3"
+                               if args.workload == "mnv4" else args.workload,
+                   "global_batch": images, "ops": len(costs),
+                   "gops_per_step": round(sum(c["ops"] for c in costs) / 1e9, 3),
+                   "gbytes_per_step": round(sum(c["bytes"] for c in costs) / 1e9, 4),
+                   "parallelism": "single GPU, batch-outer"},
+        "roofline": roof,
+        "sum_kernel_us": round(float(per_op_ns.sum()) / 1e3, 2),
+    }
+    if not args.no_secondary:
+        result["secondary"] = secondary(lib, 10)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,142 @@
+"""Random small plans that exercise every op of the INT8 vision path with
+edge-case geometry: odd channel counts, 1xN kernels, strides 1-3, dilation,
+explicit and SAME padding, K tails with nonzero weights, positive shifts,
+zero multipliers, fused post tables, batch/channel padding, slices, concat on
+every axis, resize, pooling, mean and packed outputs."""
+import numpy as np
+
+from uq_plan import Plan, Rng
+
+
+def _pick(rng, values):
+    return values[int(rng.integers(1, 0, len(values) - 1)[0])]
+
+
+def _geometry(rng, size, k, stride, dilation):
+    """Random explicit padding that leaves at least one output position."""
+    before, after = (int(v) for v in rng.integers(2, 0, 2))
+    need = (k - 1) * dilation + 1 - size
+    return before, max(after, need - before)
+
+
+def _random_lut(plan, rng):
+    return plan.lut_table(rng.int8(256).view(np.uint8))
+
+
+def conv_op(p, rng, x):
+    n, ih, iw, ic = p.shape(x)
+    oc = _pick(rng, [1, 2, 3, 4, 5, 8, 16, 17, 32, 40, 64, 96])
+    kh, kw = _pick(rng, [1, 1, 2, 3, 3, 5]), _pick(rng, [1, 1, 2, 3, 3, 5])
+    sh, sw = _pick(rng, [1, 1, 2, 3]), _pick(rng, [1, 1, 2, 3])
+    dil = _pick(rng, [1, 1, 1, 2])
+    if kh * kw * ic > 8192:
+        kh = kw = 1
+    if _pick(rng, [0, 1]):
+        padding = "same"
+        if sh != sw:
+            sw = sh
+    else:
+        pt, pb = _geometry(rng, ih, kh, sh, dil)
+        pl, pr = _geometry(rng, iw, kw, sw, dil)
+        padding = (pt, pl, pb, pr)
+    act = _pick(rng, ["none", "relu", "relu6"])
+    lut = _random_lut(p, rng) if _pick(rng, [0, 0, 1]) else None
+    kwargs = dict(k=kh, kw=kw, stride=sh, stride_w=sw, dilation=dil, padding=padding, act=act, q6=int(rng.integers(1, 1, 200)[0]),
+                  lut=lut, tail_weights=bool(_pick(rng, [0, 1])), scalar=bool(_pick(rng, [0, 0, 0, 1])),
+                  zero_mult=_pick(rng, [0.0, 0.0, 0.3]), w_sigma=_pick(rng, [3, 40, 90]))
+    lo = int(rng.integers(1, -24, -1)[0])
+    for shift in ((lo, 3), (lo, 0), (-12, -4)):
+        try:
+            return p.conv(x, oc, shift=shift, **kwargs)
+        except ValueError:
+            continue
+    raise AssertionError("unreachable")
+
+
+def dw_op(p, rng, x):
+    n, ih, iw, c = p.shape(x)
+    k = _pick(rng, [1, 2, 3, 3, 5, 5])
+    stride = _pick(rng, [1, 1, 2, 3])
+    dil = _pick(rng, [1, 1, 2])
+    if _pick(rng, [0, 1]):
+        padding = "same"
+    else:
+        pt, pb = _geometry(rng, ih, k, stride, dil)
+        pl, pr = _geometry(rng, iw, k, stride, dil)
+        padding = (pt, pl, pb, pr)
+    lut = _random_lut(p, rng) if _pick(rng, [0, 0, 1]) else None
+    lo = int(rng.integers(1, -24, -1)[0])
+    for shift in ((lo, 3), (-12, -4)):
+        try:
+            return p.depthwise(x, k=k, stride=stride, dilation=dil, padding=padding,
+                               act=_pick(rng, ["none", "relu", "relu6"]), q6=int(rng.integers(1, 1, 200)[0]),
+                               lut=lut, shift=shift, zero_mult=_pick(rng, [0.0, 0.3]),
+                               w_sigma=_pick(rng, [3, 40, 90]), bias_sigma=_pick(rng, [0, 2048, 60000]))
+        except ValueError:
+            continue
+    raise AssertionError("unreachable")
+
+
+def pool_op(p, rng, x):
+    n, ih, iw, c = p.shape(x)
+    k = _pick(rng, [1, 2, 3, 5])
+    stride = _pick(rng, [1, 2, 3])
+    if k > min(ih, iw):
+        k = min(ih, iw)
+    return p.pool(x, k, stride, kind=_pick(rng, ["max", "avg"]), padding=_pick(rng, ["same", "valid"]),
+                  act=_pick(rng, ["none", "relu"]))
+
+
+def pad_op(p, rng, x):
+    pads = [tuple(int(v) for v in rng.integers(2, 0, 2)) for _ in range(4)]
+    if _pick(rng, [0, 1]):
+        pads[0] = (0, 0)
+    return p.pad(x, pads, value=int(rng.integers(1, -128, 127)[0]))
+
+
+def slice_op(p, rng, x):
+    s = p.shape(x)
+    begin, size = [], []
+    for d in s:
+        b = int(rng.integers(1, 0, d - 1)[0])
+        size.append(int(rng.integers(1, 1, d - b)[0]))
+        begin.append(b)
+    return p.slice(x, begin, size)
+
+
+def resize_op(p, rng, x):
+    n, ih, iw, c = p.shape(x)
+    return p.resize(x, int(rng.integers(1, 1, 2 * ih + 1)[0]), int(rng.integers(1, 1, 2 * iw + 1)[0]))
+
+
+def add_op(p, rng, x):
+    other = p.lut(x, _random_lut(p, rng)) if _pick(rng, [0, 1]) else x
+    return p.add(x, other, act=_pick(rng, ["none", "relu", "relu6"]))
+
+
+def concat_op(p, rng, x):
+    other = p.lut(x, _random_lut(p, rng))
+    return p.concat(x, other, axis=_pick(rng, [0, 1, 2, 3, 3]))
+
+
+OPS = [conv_op, conv_op, conv_op, dw_op, dw_op, pool_op, pad_op, slice_op, resize_op, add_op, concat_op]
+
+
+def random_plan(seed, max_ops=4):
+    """A small random chain; returns (plan bytes, per-image input bytes)."""
+    rng = Rng(seed, 424242)
+    p = Plan(seed)
+    shape = (int(_pick(rng, [1, 1, 2])), int(rng.integers(1, 1, 12)[0]), int(rng.integers(1, 1, 12)[0]),
+             int(_pick(rng, [1, 2, 3, 4, 8, 12, 16, 24, 32, 48, 64])))
+    t = p.input(shape, zp=int(rng.integers(1, -128, 127)[0]))
+    for _ in range(int(rng.integers(1, 1, max_ops)[0])):
+        t = _pick(rng, OPS)(p, rng, t)
+    tail = _pick(rng, ["none", "mean", "pack", "copy"])
+    if tail == "mean":
+        t = p.mean(t, keepdims=bool(_pick(rng, [0, 1])), scale_ratio=float(0.3 + rng.uniform01(1)[0]))
+    elif tail == "pack":
+        extra = p.lut(t, _random_lut(p, rng))
+        t = p.pack([t, extra])
+    elif tail == "copy":
+        t = p.copy(t)
+    return p.build(t)

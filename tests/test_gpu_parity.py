@@ -1,0 +1,111 @@
+"""GPU parity: libuq_hip.so through its C ABI against the CPU oracle, byte for
+byte, on the same seeded inputs.
+
+Small image counts are compared in full; full-batch runs (256 / 512 images)
+are checked through size-independent properties: every sampled image of the
+batch equals that image run alone through the oracle, and a batch result is
+identical between the host and the device entry points."""
+import numpy as np
+import pytest
+
+import uq_plan as P
+import uq_workloads as W
+from plan_fuzz import random_plan
+from refs import oracle_run
+from uq_native import DeviceBuffer, Graph, NativeError, open_library
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return open_library()
+
+
+def _oracle(plan, x, images):
+    return oracle_run(plan, x, images, P.output_bytes(plan))
+
+
+def _assert_same(got, want, what):
+    if not np.array_equal(got, want):
+        bad = np.flatnonzero(got != want)
+        raise AssertionError(f"{what}: {bad.size} of {want.size} bytes differ; first at {bad[0]}: "
+                             f"got {got[bad[0]]} want {want[bad[0]]}")
+
+
+@pytest.mark.parametrize("name,images", [("pointwise", 1), ("pointwise", 3), ("dw3s1", 64), ("dw3s2", 64),
+                                         ("dw5s1", 64), ("dw5s2", 64), ("head", 16), ("conv3x3", 2), ("mnv4", 3)])
+def test_workload_bit_exact(lib, name, images):
+    plan, _ = W.WORKLOADS[name]()
+    x = P.random_input(plan, images, 21)
+    g = Graph(plan, lib)
+    _assert_same(g.run_batch(x, images), _oracle(plan, x, images), name)
+
+
+def test_single_image_entry_point(lib):
+    plan, _ = W.pointwise(tail_weights=True)
+    x = P.random_input(plan, 1, 4)
+    _assert_same(Graph(plan, lib).run(x), _oracle(plan, x, 1), "ug_run")
+
+
+@pytest.mark.parametrize("name,images,samples", [("mnv4", 256, (0, 137, 255)), ("head", 512, (0, 511)),
+                                                 ("conv3x3", 512, (5, 400))])
+def test_full_batch_sampled_images(lib, name, images, samples):
+    plan, _ = W.WORKLOADS[name]()
+    x = P.random_input(plan, images, 33)
+    g = Graph(plan, lib)
+    din = DeviceBuffer(lib, x.nbytes)
+    dout = DeviceBuffer(lib, images * g.output_bytes)
+    din.upload(x)
+    assert lib.ug_run_device(din.ptr, dout.ptr, images) == 0
+    y = dout.download()
+    din.free()
+    dout.free()
+    ib, ob = g.input_bytes, g.output_bytes
+    for j in samples:
+        _assert_same(y[j * ob:(j + 1) * ob], _oracle(plan, x[j * ib:(j + 1) * ib], 1), f"{name} image {j}")
+    if name == "mnv4":
+        # Host and device entry points agree on the whole batch.
+        _assert_same(g.run_batch(x, images), y, "run_batch vs run_device")
+
+
+@pytest.mark.parametrize("seed", range(80))
+def test_random_plans(lib, seed):
+    plan = random_plan(1000 + seed)
+    images = 3
+    x = P.random_input(plan, images, seed)
+    _assert_same(Graph(plan, lib).run_batch(x, images), _oracle(plan, x, images), f"random plan {1000 + seed}")
+
+
+def test_snapshot_intermediate(lib):
+    plan, _ = W.mnv4()
+    images = 2
+    x = P.random_input(plan, images, 8)
+    g = Graph(plan, lib)
+    g.run_batch(x, images)
+    recs = P.tensor_records(plan)
+    for t in (3, 40, 120):
+        nbytes = images * recs[t][1]
+        _, want = oracle_run(plan, x, images, P.output_bytes(plan), snap=t, snap_bytes=nbytes)
+        _assert_same(g.snapshot_images(t, nbytes), want, f"snapshot tensor {t}")
+
+
+def test_profile_counters(lib):
+    plan, _ = W.pointwise()
+    g = Graph(plan, lib)
+    g.profile(1)
+    x = P.random_input(plan, 1, 1)
+    for _ in range(3):
+        g.run(x)
+    c = g.profile(2)
+    assert c[0] == 3 and c[1] > 0 and c[2] > 0
+
+
+def test_bad_sizes_rejected(lib):
+    plan, _ = W.pointwise()
+    g = Graph(plan, lib)
+    x = np.zeros(g.input_bytes + 1, np.int8)
+    y = np.zeros(g.output_bytes, np.int8)
+    assert lib.ug_run(x.ctypes.data, x.nbytes, y.ctypes.data, y.nbytes) == 22
+    with pytest.raises(NativeError):
+        g.run_batch(np.zeros(3 * g.input_bytes, np.int8), 2)

@@ -1,0 +1,897 @@
+/* Plain-C graph host of libuq_hip.so: plan validation, load-time preparation
+ * of device tables, and an in-order executor that enqueues gfx950 kernels
+ * through the thin C ABI of uqk.h.
+ *
+ * The plan format, the validation rules and their error codes are the
+ * reference's interface (runtime/graph.c:50-262, runtime/qnn.c:209-252), so a
+ * plan is accepted or rejected here exactly as the reference loader would,
+ * with the same code; the checks run in the reference's order because the
+ * first failing check decides the code. Execution differs by design: every
+ * activation tensor owns a device buffer sized for a whole batch of stacked
+ * images, constants are uploaded once, and each op is one kernel launch (or a
+ * device copy) on one HIP stream.
+ */
+#include "uq_graph.h"
+#include "uqk.h"
+#include <stdlib.h>
+#include <string.h>
+
+#define UG_MAGIC 0x55474e31u
+#define UG_MAX_T 1024u
+#define UG_MAX_OP 512u
+#define UG_ARENA (16u * 1024u * 1024u)
+#define UG_MAX_WORK 2000000000ULL
+#define UQ_HEAD 20
+#define UQ_MAX_K 8192
+#define UQ_MAX_C 2048
+
+/* Record layouts of graph.h:15-17 (the plan ABI). */
+typedef struct { uint32_t magic, version, nt, no, arena_bytes, input, output, reserved; } Header;
+typedef struct { uint32_t offset, bytes, type, rank, d[4], flags, reserved[3]; } Tensor;
+typedef struct { uint32_t code, a, b, out, p[4]; } Op;
+
+static struct {
+    int ready, profile_enabled, stream_active, vision_only;
+    Header h;
+    Tensor ts[UG_MAX_T];
+    Op ops[UG_MAX_OP];
+    uint8_t *arena;              /* host copy of the plan arena */
+    uint8_t *dev_arena;          /* device copy of the plan arena (constants) */
+    uint8_t *dev_prep;           /* device pool of prepared per-op tables */
+    uint8_t *act[UG_MAX_T];      /* device activation buffers, capacity images each */
+    uint8_t *ptr[UG_MAX_T];      /* per-run tensor addresses */
+    uint32_t capacity, last_images;
+    UQKSpatial sp[UG_MAX_OP];
+    uint64_t ticks[UG_MAX_OP + 2];
+} G;
+
+static uint32_t width(uint32_t t) { return t == 1 || t == 4 ? 4 : t == 2 || t == 3 ? 1 : 0; }
+
+static int same(const Tensor *a, const Tensor *b)
+{
+    if (a->type != b->type || a->rank != b->rank) return 0;
+    for (uint32_t i = 0; i < a->rank; i++)
+        if (a->d[i] != b->d[i]) return 0;
+    return 1;
+}
+
+/* Scalar, last-axis vector, or equal shape (graph.c:33-40). */
+static int broadcast(const Tensor *a, const Tensor *b)
+{
+    if (a->type != b->type || b->rank > a->rank) return 0;
+    for (uint32_t i = 0; i < b->rank; i++)
+        if (b->d[i] != 1 && b->d[i] != a->d[a->rank - b->rank + i]) return 0;
+    if (b->bytes == width(b->type)) return 1;
+    if (b->bytes == a->d[a->rank - 1] * width(b->type)) {
+        for (uint32_t i = 0; i + 1 < b->rank; i++)
+            if (b->d[i] != 1) return 0;
+        return 1;
+    }
+    return same(a, b);
+}
+
+/* Host twin of the device requantiser, used only by the load-time bound
+ * proof (qnn.c:246-249 needs the scaled endpoints). */
+static int32_t scale_host(int32_t v, int32_t m, int shift)
+{
+    if (shift > 0) v = (int32_t)((uint32_t)v << shift);
+    int64_t p = (int64_t)v * m;
+    int32_t h = (int32_t)((p + ((int64_t)1 << 30)) >> 31);
+    if (shift >= 0) return h;
+    unsigned s = (unsigned)-shift;
+    uint32_t mask = ((uint32_t)1 << s) - 1;
+    return (h >> s) + (((uint32_t)h & mask) > ((mask >> 1) + (uint32_t)(h < 0)));
+}
+
+static int packed_weight(const int8_t *w, uint32_t n, uint32_t k, uint32_t kp)
+{
+    return w[(size_t)(n / 4) * kp * 4 + (size_t)(k / 8) * 32 + (n % 4) * 8 + k % 8];
+}
+
+/* Spatial-op rules of qnn.c:209-252 (codes 14-17), including the per-channel
+ * int32 bound proof over unsigned inputs in [0, 255]. */
+static int check_spatial(const Op *o, const Tensor *a, const Tensor *b, const Tensor *z, const Tensor *t,
+                         const int32_t *q, const int8_t *w, uint64_t *work)
+{
+    if (a->type != 3 || z->type != 3 || !t->flags || t->type != 4 || t->bytes < UQ_HEAD * 4 ||
+        ((o->code != 14 && o->code != 15) && o->p[1]) || o->p[2] || o->p[3])
+        return 18;
+    if (q[12] < -128 || q[12] > 127 || q[13] < -128 || q[13] > 127 || q[14] < -128 || q[15] > 127 || q[14] > q[15] ||
+        q[19] < 0 || q[19] > 1)
+        return 18;
+    if (o->code == 17) {
+        if (q[13] != -128 || q[14] != -128 || q[15] != 127 || a->rank != z->rank || a->bytes != z->bytes || !a->rank ||
+            q[16] != (int32_t)a->d[a->rank - 1] || q[16] < 1 || q[16] > UQ_MAX_C || t->bytes != (UQ_HEAD + 256) * 4)
+            return 18;
+        for (unsigned i = 0; i < 256; i++)
+            if (q[UQ_HEAD + i] < 0 || q[UQ_HEAD + i] > (1 << 24)) return 18;
+        for (unsigned d = 0; d < a->rank; d++)
+            if (a->d[d] != z->d[d]) return 18;
+        if (q[UQ_HEAD] != (1 << 24)) return 18;
+        *work += a->bytes;
+        return 0;
+    }
+    if (a->rank != 4 || z->rank != 4 || a->d[0] != z->d[0] || q[16] != (int32_t)a->d[3] || q[17] != (int32_t)z->d[3] ||
+        q[16] < 1 || q[16] > UQ_MAX_C || q[17] < 1 || q[17] > UQ_MAX_C)
+        return 18;
+    for (unsigned i = 0; i < 6; i++)
+        if (q[i] < 1 || q[i] > 4096) return 18;
+    for (unsigned i = 6; i < 12; i++)
+        if (q[i] < 0 || q[i] > 4096) return 18;
+    int64_t hh = (int64_t)a->d[1] + q[6] + q[8] - (int64_t)(q[0] - 1) * q[4] - 1;
+    int64_t ww = (int64_t)a->d[2] + q[7] + q[9] - (int64_t)(q[1] - 1) * q[5] - 1;
+    if (hh < 0 || ww < 0 || hh / q[2] + 1 != q[10] || ww / q[3] + 1 != q[11] || q[10] != (int32_t)z->d[1] ||
+        q[11] != (int32_t)z->d[2])
+        return 18;
+    uint64_t area = (uint64_t)q[0] * q[1], rows = (uint64_t)z->d[0] * z->d[1] * z->d[2];
+    if (o->code == 16) {
+        if (q[16] != q[17] || q[12] != q[13] || q[4] != 1 || q[5] != 1 || area > 8192 || t->bytes != UQ_HEAD * 4) return 18;
+        if (q[6] >= q[0] || q[7] >= q[1] || (q[10] - 1) * (int64_t)q[2] - q[6] >= a->d[1] ||
+            (q[11] - 1) * (int64_t)q[3] - q[7] >= a->d[2])
+            return 18;
+        *work += rows * area * q[16];
+        return 0;
+    }
+    uint64_t k = area * (o->code == 15 ? 1 : (uint64_t)q[16]);
+    if (k > UQ_MAX_K || q[18] != (int32_t)((k + 7) & ~7ULL) || !b->flags || b->type != 3 ||
+        t->bytes != (uint32_t)(UQ_HEAD + 3 * q[17]) * 4)
+        return 18;
+    if (o->code == 15) {
+        if (q[16] != q[17] || b->bytes != area * q[17]) return 18;
+    } else if (b->bytes != (uint32_t)((q[17] + 3) & ~3) * q[18])
+        return 18;
+    const int oc = q[17];
+    for (int c = 0; c < oc; c++) {
+        int shift = q[UQ_HEAD + 2 * oc + c], m = q[UQ_HEAD + oc + c];
+        if (m < 0 || shift < -31 || shift > 15) return 18;
+        int64_t lo = q[UQ_HEAD + c], hi = lo;
+        unsigned terms = o->code == 15 ? (unsigned)k : (unsigned)q[18];
+        for (unsigned j = 0; j < terms; j++) {
+            int v = o->code == 15 ? w[j * oc + c] : packed_weight(w, (uint32_t)c, j, terms);
+            if (v < 0) lo += 255 * v;
+            else hi += 255 * v;
+        }
+        int64_t factor = (int64_t)1 << (shift > 0 ? shift : 0);
+        if (lo * factor < INT32_MIN || hi * factor > INT32_MAX) return 18;
+        if ((int64_t)scale_host((int32_t)lo, m, shift) + q[13] < INT32_MIN ||
+            (int64_t)scale_host((int32_t)hi, m, shift) + q[13] > INT32_MAX)
+            return 18;
+    }
+    *work += rows * k * q[17];
+    return 0;
+}
+
+/* Structural validation of a whole plan: graph.c:50-216. Fills G.h/ts/ops. */
+static int validate(const uint8_t *p, uint32_t len)
+{
+    Header *h = &G.h;
+    if (!p || len < sizeof(Header)) return 10;
+    memcpy(h, p, sizeof(Header));
+    if (h->magic != UG_MAGIC || h->version < 1 || h->version > 3 || !h->nt || h->nt > UG_MAX_T || !h->no ||
+        h->no > UG_MAX_OP || !h->arena_bytes || h->arena_bytes > UG_ARENA || h->input >= h->nt || h->output >= h->nt ||
+        (h->version == 1 ? h->reserved != 0 : h->reserved > 1))
+        return 11;
+    uint32_t meta = (uint32_t)sizeof(Header) + h->nt * (uint32_t)sizeof(Tensor) + h->no * (uint32_t)sizeof(Op);
+    if (len != meta + h->arena_bytes) return 12;
+    memcpy(G.ts, p + sizeof(Header), h->nt * sizeof(Tensor));
+    memcpy(G.ops, p + sizeof(Header) + h->nt * sizeof(Tensor), h->no * sizeof(Op));
+    const uint8_t *arena = p + meta;
+    static unsigned char defined[UG_MAX_T];
+    static int birth[UG_MAX_T], death[UG_MAX_T];
+    memset(defined, 0, sizeof defined);
+    uint32_t end = 0;
+    for (uint32_t i = 0; i < h->nt; i++) {
+        Tensor *t = G.ts + i;
+        uint32_t w = width(t->type);
+        uint64_t count = 1;
+        if (!w || t->rank > 4 || t->offset % 128 || (h->version < 3 && t->offset < end) || t->offset > h->arena_bytes ||
+            t->flags > 1 || t->reserved[0] || t->reserved[1] || t->reserved[2])
+            return 13;
+        for (uint32_t d = 0; d < t->rank; d++) {
+            if (!t->d[d] || t->d[d] > UG_ARENA) return 13;
+            count *= t->d[d];
+            if (count > UG_ARENA) return 13;
+        }
+        if (count * w != t->bytes || t->bytes > h->arena_bytes - t->offset) return 13;
+        end = t->offset + t->bytes;
+        defined[i] = (unsigned char)t->flags;
+        birth[i] = -1;
+        death[i] = t->flags ? (int)h->no : -1;
+    }
+    if (G.ts[h->input].flags) return 14;
+    defined[h->input] = 1;
+    uint64_t work = 0;
+    int vision_only = 1, parallel_vision = 0;
+    for (uint32_t i = 0; i < h->no; i++) {
+        const Op *o = G.ops + i;
+        if (o->code != 5 && o->code != 10 && (o->code < 14 || o->code > 28)) vision_only = 0;
+        if (o->a >= h->nt || o->b >= h->nt || o->out >= h->nt || !defined[o->a] || defined[o->out]) return 15;
+        const Tensor *a = G.ts + o->a, *b = G.ts + o->b, *z = G.ts + o->out;
+        const uint32_t c = o->code;
+        if (c == 1 || c == 6 || c == 8 || c == 9) {
+            int integer = c == 6 || c == 9, packed = c == 8 || c == 9;
+            if (packed && h->version < 2) return 16;
+            if (!defined[o->b] || !b->flags || a->rank != 2 || b->rank != 2 || z->rank != 2 || a->d[1] != b->d[1] ||
+                z->d[0] != a->d[0] || (packed ? ((z->d[1] + 3) / 4 * 4 != b->d[0]) : z->d[1] != b->d[0]))
+                return 16;
+            if (!integer && (a->type != 1 || b->type != 1 || z->type != 1)) return 16;
+            if (integer && (a->type != 2 || b->type != 3 || z->type != 4 || a->d[1] > 8192 || o->p[0] > 255 ||
+                            (int32_t)o->p[1] < -128 || (int32_t)o->p[1] > 127))
+                return 16;
+            if (integer && (o->p[3] != 1 || o->p[2] >= h->nt || !defined[o->p[2]] || !G.ts[o->p[2]].flags ||
+                            G.ts[o->p[2]].type != 4 || G.ts[o->p[2]].bytes != z->d[1] * 4))
+                return 16;
+            if (c == 8 && (o->p[0] > 1 || o->p[1] || o->p[2] || o->p[3])) return 16;
+            if (c == 9 && a->d[1] % 8) return 16;
+            work += (uint64_t)a->d[0] * a->d[1] * z->d[1];
+        } else if (c == 2 || c == 3) {
+            if (!defined[o->b] || !same(a, z) || !broadcast(a, b) || (a->type != 1 && a->type != 4)) return 17;
+            work += a->bytes / width(a->type);
+        } else if (c == 4) {
+            if (!same(a, z) || (a->type != 1 && a->type != 4)) return 18;
+            work += a->bytes / 4;
+        } else if (c == 5) {
+            if (a->type != z->type || a->bytes != z->bytes) return 18;
+            work += a->bytes;
+        } else if (c == 7) {
+            if (a->type != 4 || z->type != 1 || a->bytes != z->bytes) return 18;
+            work += a->bytes / 4;
+        } else if (c == 10) {
+            if (a->rank != z->rank || a->type != z->type || a->bytes != z->bytes) return 18;
+            unsigned seen = 0;
+            for (unsigned d = 0; d < a->rank; d++) {
+                unsigned q = o->p[d];
+                if (q >= a->rank || (seen & (1u << q)) || z->d[d] != a->d[q]) return 18;
+                seen |= 1u << q;
+            }
+            work += z->bytes;
+        } else if (c == 11 || c == 12) {
+            if (a->rank != 4 || a->type != 1 || z->type != 1 || !defined[o->b] || !b->flags || b->type != 4 || b->bytes != 48)
+                return 18;
+            int32_t q[12];
+            memcpy(q, arena + b->offset, 48);
+            for (unsigned d = 0; d < 6; d++)
+                if (q[d] < 1 || q[d] > 4096) return 18;
+            for (unsigned d = 6; d < 12; d++)
+                if (q[d] < 0 || q[d] > 4096) return 18;
+            int64_t hh = (int64_t)a->d[1] + q[6] + q[8] - (q[0] - 1) * (int64_t)q[4] - 1;
+            int64_t ww = (int64_t)a->d[2] + q[7] + q[9] - (q[1] - 1) * (int64_t)q[5] - 1;
+            if (hh < 0 || ww < 0 || hh / q[2] + 1 != q[10] || ww / q[3] + 1 != q[11]) return 18;
+            uint64_t rows = (uint64_t)a->d[0] * q[10] * q[11], k = (uint64_t)q[0] * q[1] * a->d[3];
+            if (c == 11) {
+                if (z->rank != 2 || z->d[0] != rows || z->d[1] != k) return 18;
+            } else if (z->rank != 4 || z->d[0] != a->d[0] || z->d[1] != (uint32_t)q[10] || z->d[2] != (uint32_t)q[11] ||
+                       z->d[3] != a->d[3])
+                return 18;
+            work += rows * k;
+        } else if (c == 13) {
+            if (!same(a, z) || a->type != 1 || !a->rank) return 18;
+            work += a->bytes / 4;
+        } else if (c >= 14 && c <= 17) {
+            if (h->version < 2 || o->p[0] >= h->nt || !defined[o->p[0]] || !defined[o->b]) return 18;
+            const Tensor *t = G.ts + o->p[0];
+            int rc = check_spatial(o, a, b, z, t, (const int32_t *)(arena + t->offset), (const int8_t *)(arena + b->offset), &work);
+            if (rc) return rc;
+            if (o->p[1]) {
+                unsigned id = o->p[1] - 1;
+                if (id >= h->nt || !G.ts[id].flags || G.ts[id].type != 2 || G.ts[id].bytes != 256) return 18;
+                death[id] = (int)i;
+                work += z->bytes;
+            }
+            if ((c == 14 || c == 15) && z->bytes >= 2048 && (uint64_t)z->d[0] * z->d[1] * z->d[2] >= 8) parallel_vision = 1;
+        } else if (c == 18) {
+            if (h->version < 2 || !defined[o->b] || a->type != 3 || !same(a, b) || !same(a, z) || o->p[0] >= h->nt || o->p[1] ||
+                o->p[2] || o->p[3])
+                return 18;
+            const Tensor *t = G.ts + o->p[0];
+            if (!t->flags || t->type != 4 || t->bytes != 520 * 4) return 18;
+            const int32_t *q = (const int32_t *)(arena + t->offset);
+            if (q[0] < 0 || q[1] < -31 || q[1] > 0 || q[2] < -128 || q[2] > 127 || q[3] < -128 || q[4] > 127 || q[3] > q[4] ||
+                q[5] || q[6] || q[7])
+                return 18;
+            for (unsigned j = 8; j < 520; j++)
+                if (q[j] < -267386880 || q[j] > 267386880) return 18;
+            work += z->bytes;
+        } else if (c == 19) {
+            if (h->version < 2 || !b->flags || b->type != 4 || !b->bytes || b->bytes > 32 * 4 || b->bytes % 4 || z->type != 3 ||
+                z->rank != 1 || o->p[0] || o->p[1] || o->p[2] || o->p[3])
+                return 18;
+            const uint32_t *list = (const uint32_t *)(arena + b->offset);
+            uint64_t total = 0;
+            if (list[0] != o->a) return 18;
+            for (unsigned j = 0; j < b->bytes / 4; j++) {
+                unsigned id = list[j];
+                if (id >= h->nt || !defined[id] || (G.ts[id].type != 2 && G.ts[id].type != 3)) return 18;
+                total += G.ts[id].bytes;
+                death[id] = (int)i;
+            }
+            if (total != z->bytes) return 18;
+            work += total;
+        } else if (c == 20) {
+            unsigned axis = o->p[0];
+            if (h->version < 2 || !defined[o->b] || a->type != 3 || b->type != 3 || z->type != 3 || a->rank != b->rank ||
+                a->rank != z->rank || axis >= a->rank || o->p[1] || o->p[2] || o->p[3])
+                return 18;
+            for (unsigned d = 0; d < a->rank; d++) {
+                if (d == axis) {
+                    if ((uint64_t)a->d[d] + b->d[d] != z->d[d]) return 18;
+                } else if (a->d[d] != b->d[d] || a->d[d] != z->d[d])
+                    return 18;
+            }
+            work += z->bytes;
+        } else if (c == 21) {
+            if (h->version < 2 || a->type != 3 || z->type != 3 || a->rank != 4 || z->rank != 4 || a->d[0] != z->d[0] ||
+                a->d[3] != z->d[3] || !b->flags || b->type != 4 || b->bytes != (z->d[1] + z->d[2]) * 4 || o->p[0] || o->p[1] ||
+                o->p[2] || o->p[3])
+                return 18;
+            const uint32_t *q = (const uint32_t *)(arena + b->offset);
+            uint32_t row = a->d[2] * a->d[3], batch = a->d[1] * row;
+            for (unsigned d = 0; d < z->d[1]; d++)
+                if (q[d] >= batch || q[d] % row) return 18;
+            for (unsigned d = 0; d < z->d[2]; d++)
+                if (q[z->d[1] + d] >= row || q[z->d[1] + d] % a->d[3]) return 18;
+            work += z->bytes;
+        } else if (c == 22) {
+            if (h->version < 2 || (a->type != 2 && a->type != 3) || (z->type != 2 && z->type != 3) || a->rank != z->rank ||
+                a->bytes != z->bytes || !b->flags || b->type != 2 || b->bytes != 256 || o->p[0] || o->p[1] || o->p[2] || o->p[3])
+                return 18;
+            for (unsigned d = 0; d < a->rank; d++)
+                if (a->d[d] != z->d[d]) return 18;
+            work += z->bytes;
+        } else if (c == 23) {
+            if (h->version < 2 || a->type != 3 || z->type != 3 || a->rank != 4 || z->rank != 4 || !b->flags || b->type != 4 ||
+                b->bytes != 32 || (int32_t)o->p[0] < -128 || (int32_t)o->p[0] > 127 || o->p[1] || o->p[2] || o->p[3])
+                return 18;
+            const int32_t *q = (const int32_t *)(arena + b->offset);
+            for (unsigned d = 0; d < 4; d++)
+                if (q[d * 2] < 0 || q[d * 2] > 4096 || q[d * 2 + 1] < 0 || q[d * 2 + 1] > 4096 ||
+                    (uint64_t)a->d[d] + q[d * 2] + q[d * 2 + 1] != z->d[d])
+                    return 18;
+            work += z->bytes;
+        } else if (c == 24) {
+            if (h->version < 2 || a->type != 3 || z->type != 3 || a->rank != 4 || (z->rank != 2 && z->rank != 4) || !b->flags ||
+                b->type != 4 || b->bytes != 20 || o->p[0] || o->p[1] || o->p[2] || o->p[3])
+                return 18;
+            if (z->d[0] != a->d[0] || z->d[z->rank - 1] != a->d[3] || (z->rank == 4 && (z->d[1] != 1 || z->d[2] != 1))) return 18;
+            const int32_t *q = (const int32_t *)(arena + b->offset);
+            if (q[0] < 1 || (uint64_t)a->d[1] * a->d[2] != (uint32_t)q[0] || q[1] < -128 || q[1] > 127 || q[2] < -128 ||
+                q[2] > 127 || q[3] < 0 || q[4] < -31 || q[4] > 30)
+                return 18;
+            uint64_t bound = (uint64_t)q[0] * (q[1] >= 0 ? 128 + q[1] : 127 - q[1]);
+            if ((bound << (q[4] > 0 ? q[4] : 0)) > 2147483520u) return 18;
+            work += a->bytes;
+        } else if (c == 25 || c == 27) {
+            if (h->version < 2 || a->type != 3 || b->type != 3 || z->type != 3 || !defined[o->b] || o->p[0] >= h->nt || o->p[1] ||
+                o->p[2] || o->p[3])
+                return 18;
+            const Tensor *t = G.ts + o->p[0];
+            if (!t->flags || t->type != 4 || t->bytes != 28) return 18;
+            const int32_t *q = (const int32_t *)(arena + t->offset);
+            for (unsigned j = 0; j < 3; j++)
+                if (q[j] < -128 || q[j] > 127) return 18;
+            if (q[3] < 0 || q[4] < -31 || q[4] > 15) return 18;
+            uint64_t k = 1;
+            if (c == 25) {
+                if (!same(a, b) || !same(a, z) || q[5] < -128 || q[6] > 127 || q[5] > q[6]) return 18;
+                work += z->bytes;
+            } else {
+                if (a->rank != 3 || b->rank != 3 || z->rank != 3 || q[5] < 0 || q[5] > 1 || q[6] < 0 || q[6] > 1 ||
+                    a->d[0] != b->d[0] || a->d[0] != z->d[0])
+                    return 18;
+                unsigned m = a->d[q[5] ? 2 : 1], n = b->d[q[6] ? 1 : 2];
+                k = a->d[q[5] ? 1 : 2];
+                if (k != b->d[q[6] ? 2 : 1] || k > 8192 || n > 2048 || z->d[1] != m || z->d[2] != n) return 18;
+                work += (uint64_t)z->bytes * k;
+            }
+            if (k * 65025 * (1ULL << (q[4] > 0 ? q[4] : 0)) > 2147483520u) return 18;
+        } else if (c == 26) {
+            if (h->version < 2 || a->type != 3 || z->type != 3 || a->rank != z->rank || !a->rank) return 18;
+            for (unsigned d = 0; d < 4; d++) {
+                if (d >= a->rank) {
+                    if (o->p[d]) return 18;
+                } else if ((uint64_t)o->p[d] + z->d[d] > a->d[d])
+                    return 18;
+            }
+            work += z->bytes;
+        } else if (c == 28) {
+            if (h->version < 2 || a->type != 3 || !same(a, z) || !a->rank || a->d[a->rank - 1] > 2048 || !b->flags ||
+                b->type != 4 || b->bytes != 257 * 4 || o->p[0] || o->p[1] || o->p[2] || o->p[3])
+                return 18;
+            const int32_t *q = (const int32_t *)(arena + b->offset);
+            if (q[0] != (int32_t)a->d[a->rank - 1] || q[1] != 2147483647) return 18;
+            for (unsigned d = 2; d <= 256; d++)
+                if (q[d] < 0 || q[d] > q[d - 1]) return 18;
+            work += z->bytes;
+        } else
+            return 19;
+        if (work > UG_MAX_WORK) return 20;
+        death[o->a] = (int)i;
+        death[o->b] = (int)i;
+        birth[o->out] = (int)i;
+        death[o->out] = (int)i;
+        if ((c >= 14 && c <= 18) || c == 25 || c == 27) death[o->p[0]] = (int)i;
+        if (c == 6 || c == 9) death[o->p[2]] = (int)i;
+        defined[o->out] = 1;
+    }
+    G.vision_only = vision_only && parallel_vision;
+    if (!defined[h->output]) return 21;
+    if (h->version == 3) {
+        death[h->output] = (int)h->no;
+        for (unsigned x = 0; x < h->nt; x++) {
+            if (G.ts[x].flags) {
+                birth[x] = -1;
+                death[x] = (int)h->no;
+            }
+            if (!defined[x]) return 15;
+        }
+        for (unsigned x = 0; x < h->nt; x++)
+            for (unsigned y = x + 1; y < h->nt; y++) {
+                int mem = G.ts[x].offset < G.ts[y].offset + G.ts[y].bytes && G.ts[y].offset < G.ts[x].offset + G.ts[x].bytes;
+                int live = birth[x] <= death[y] && birth[y] <= death[x];
+                if (mem && live) return 25;
+            }
+    }
+    return 0;
+}
+
+/* Codes this library executes on the GPU: the INT8 vision path. */
+static int supported(uint32_t code)
+{
+    switch (code) {
+    case 5: case 14: case 15: case 16: case 18: case 19: case 20: case 21: case 22: case 23: case 24: case 26: return 1;
+    default: return 0;
+    }
+}
+
+static void release_device(void)
+{
+    for (uint32_t i = 0; i < UG_MAX_T; i++) {
+        uqk_free(G.act[i]);
+        G.act[i] = NULL;
+    }
+    uqk_free(G.dev_arena);
+    uqk_free(G.dev_prep);
+    G.dev_arena = G.dev_prep = NULL;
+    G.capacity = 0;
+    G.last_images = 0;
+}
+
+static uint32_t round_up(uint32_t v, uint32_t m) { return (v + m - 1) / m * m; }
+
+/* N tile count per block (16 channels each): the least padded choice. */
+static int choose_nt(int oc)
+{
+    static const int opts[4] = {8, 6, 4, 2};
+    int best = 8, waste = 1 << 30;
+    for (int i = 0; i < 4; i++) {
+        int bn = 16 * opts[i], pad = (oc + bn - 1) / bn * bn - oc;
+        if (pad < waste) { waste = pad; best = opts[i]; }
+    }
+    return best;
+}
+
+typedef struct { size_t w, epi, kmap, end; } Layout;
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+/* Sizes of one spatial op's prepared tables in the device pool. */
+static Layout spatial_layout(const Op *o, size_t at)
+{
+    const int32_t *q = (const int32_t *)(G.arena + G.ts[o->p[0]].offset);
+    Layout L = {at, at, at, at};
+    int oc = q[17];
+    if (o->code == 14) {
+        int K = q[0] * q[1] * q[16], kpad = (int)round_up((uint32_t)K, 64), nt = choose_nt(oc);
+        int oc_pad = (int)round_up((uint32_t)oc, (uint32_t)(16 * nt));
+        int ic = q[16], group = ic % 16 == 0 ? 16 : ic % 4 == 0 ? 4 : 1;
+        L.w = at;
+        L.epi = align256(L.w + (size_t)oc_pad * kpad);
+        L.kmap = align256(L.epi + (size_t)oc * 16);
+        L.end = align256(L.kmap + (size_t)(K / group + 1) * 16);
+    } else if (o->code == 15) {
+        L.epi = at;
+        L.end = align256(L.epi + (size_t)oc * 16);
+    }
+    return L;
+}
+
+/* Build one spatial op's descriptor and host-side tables (graph-time work of
+ * the reference's prepare step, qnn.c:388-501, re-targeted at the GPU). */
+static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
+{
+    const Op *o = G.ops + i;
+    const Tensor *a = G.ts + o->a;
+    const int32_t *q = (const int32_t *)(G.arena + G.ts[o->p[0]].offset);
+    UQKSpatial *d = G.sp + i;
+    memset(d, 0, sizeof *d);
+    d->ih = (int32_t)a->d[1]; d->iw = (int32_t)a->d[2]; d->ic = q[16];
+    d->oh = q[10]; d->ow = q[11]; d->oc = q[17];
+    d->kh = q[0]; d->kw = q[1]; d->sh = q[2]; d->sw = q[3]; d->dh = q[4]; d->dw = q[5];
+    d->pt = q[6]; d->pl = q[7];
+    d->xz = q[12]; d->yz = q[13]; d->lo = q[14]; d->hi = q[15];
+    d->is_max = o->code == 16 ? q[19] : 0;
+    d->vec = d->oc % 16 == 0 ? 16 : d->oc % 4 == 0 ? 4 : 1;
+    if (o->code != 16 && o->p[1]) d->lut = G.dev_arena + G.ts[o->p[1] - 1].offset;
+    const int oc = q[17];
+    const int32_t *bias = q + UQ_HEAD, *mult = bias + oc, *shift = mult + oc;
+    const int8_t *w = (const int8_t *)(G.arena + G.ts[o->b].offset);
+    if (o->code == 14) {
+        int K = q[0] * q[1] * q[16], kp = q[18], kpad = (int)round_up((uint32_t)K, 64), nt = choose_nt(oc);
+        int oc_pad = (int)round_up((uint32_t)oc, (uint32_t)(16 * nt)), ic = q[16];
+        int pointwise = q[0] == 1 && q[1] == 1 && q[2] == 1 && q[3] == 1 && !q[6] && !q[7] && !q[8] && !q[9];
+        int group = ic % 16 == 0 ? 16 : ic % 4 == 0 ? 4 : 1;
+        d->K = K; d->kpad = kpad; d->oc_pad = oc_pad; d->nt = nt; d->rb = 2;
+        d->mode = pointwise && group == 16 ? UQK_PW : group == 16 ? UQK_G16 : group == 4 ? UQK_G4 : UQK_G1;
+        int8_t *wt = (int8_t *)host_pool + L->w;
+        int32_t *epi = (int32_t *)(host_pool + L->epi);
+        int32_t *kmap = (int32_t *)(host_pool + L->kmap);
+        memset(wt, 0, (size_t)oc_pad * kpad);
+        for (int n = 0; n < oc; n++) {
+            int64_t all = 0, tail = 0;
+            for (int k = 0; k < kp; k++) {
+                int v = packed_weight(w, (uint32_t)n, (uint32_t)k, (uint32_t)kp);
+                all += v;
+                if (k < K) wt[(size_t)n * kpad + k] = (int8_t)v;
+                else tail += v;
+            }
+            /* u = s + 128 on every column; the K tail holds xz + 128. */
+            int64_t b2 = (int64_t)bias[n] + 128 * all + (int64_t)q[12] * tail;
+            epi[4 * n + 0] = (int32_t)(uint32_t)(uint64_t)b2;
+            epi[4 * n + 1] = mult[n];
+            epi[4 * n + 2] = shift[n];
+            epi[4 * n + 3] = 0;
+        }
+        for (int g = 0; g < K / group; g++) {
+            int k = g * group, t = k / ic, c = k % ic, ky = t / q[1], kx = t % q[1];
+            kmap[4 * g + 0] = ky * q[4];
+            kmap[4 * g + 1] = kx * q[5];
+            kmap[4 * g + 2] = c;
+            kmap[4 * g + 3] = 0;
+        }
+        d->w = G.dev_prep + L->w;
+        d->epi = G.dev_prep + L->epi;
+        d->kmap = G.dev_prep + L->kmap;
+    } else if (o->code == 15) {
+        int taps = q[0] * q[1];
+        int32_t *epi = (int32_t *)(host_pool + L->epi);
+        for (int c = 0; c < oc; c++) {
+            int64_t all = 0;
+            for (int t = 0; t < taps; t++) all += w[t * oc + c];
+            epi[4 * c + 0] = (int32_t)(uint32_t)(uint64_t)((int64_t)bias[c] + 128 * all);
+            epi[4 * c + 1] = mult[c];
+            epi[4 * c + 2] = shift[c];
+            epi[4 * c + 3] = 0;
+        }
+        d->w = G.dev_arena + G.ts[o->b].offset;
+        d->epi = G.dev_prep + L->epi;
+    }
+}
+
+static int prepare_device(void)
+{
+    if (uqk_init()) return 24;
+    G.dev_arena = uqk_malloc(G.h.arena_bytes);
+    if (!G.dev_arena) return 24;
+    size_t at = 0;
+    static Layout layouts[UG_MAX_OP];
+    for (uint32_t i = 0; i < G.h.no; i++) {
+        const Op *o = G.ops + i;
+        if (o->code == 14 || o->code == 15 || o->code == 16) {
+            layouts[i] = spatial_layout(o, at);
+            at = layouts[i].end;
+        }
+    }
+    uint8_t *host_pool = calloc(at + 256, 1);
+    if (!host_pool) return 24;
+    G.dev_prep = uqk_malloc(at + 256);
+    if (!G.dev_prep) { free(host_pool); return 24; }
+    for (uint32_t i = 0; i < G.h.no; i++) {
+        const Op *o = G.ops + i;
+        if (o->code == 14 || o->code == 15 || o->code == 16) prepare_spatial(i, layouts + i, host_pool);
+    }
+    int rc = uqk_h2d(G.dev_arena, G.arena, G.h.arena_bytes);
+    if (!rc) rc = uqk_h2d(G.dev_prep, host_pool, at + 256);
+    if (!rc) rc = uqk_sync();
+    free(host_pool);
+    if (!rc) rc = uqk_events(G.h.no + 1);
+    return rc ? 24 : 0;
+}
+
+int ug_load(const void *blob, uint32_t len)
+{
+    G.ready = 0;
+    G.profile_enabled = 0;
+    G.stream_active = 0;
+    release_device();
+    int rc = validate((const uint8_t *)blob, len);
+    if (rc) return rc;
+    for (uint32_t i = 0; i < G.h.no; i++)
+        if (!supported(G.ops[i].code)) return 19;
+    free(G.arena);
+    G.arena = malloc(G.h.arena_bytes);
+    if (!G.arena) return 24;
+    uint32_t meta = (uint32_t)sizeof(Header) + G.h.nt * (uint32_t)sizeof(Tensor) + G.h.no * (uint32_t)sizeof(Op);
+    memcpy(G.arena, (const uint8_t *)blob + meta, G.h.arena_bytes);
+    rc = prepare_device();
+    if (rc) {
+        release_device();
+        return rc;
+    }
+    memset(G.ticks, 0, sizeof G.ticks);
+    G.ready = 1;
+    return 0;
+}
+
+uint32_t ug_input_bytes(void) { return G.ready ? G.ts[G.h.input].bytes : 0; }
+uint32_t ug_output_bytes(void) { return G.ready ? G.ts[G.h.output].bytes : 0; }
+uint32_t ug_op_count(void) { return G.ready ? G.h.no : 0; }
+
+static int ensure_capacity(uint32_t images)
+{
+    if (images <= G.capacity) return 0;
+    if (uqk_sync()) return 24;
+    for (uint32_t t = 0; t < G.h.nt; t++) {
+        uqk_free(G.act[t]);
+        G.act[t] = NULL;
+    }
+    G.capacity = 0;
+    for (uint32_t t = 0; t < G.h.nt; t++) {
+        if (G.ts[t].flags) continue;
+        G.act[t] = uqk_malloc((size_t)images * G.ts[t].bytes);
+        if (!G.act[t]) return 24;
+    }
+    G.capacity = images;
+    return 0;
+}
+
+/* Enqueue every op of the plan for `images` stacked images on the library
+ * stream. Tensor addresses come from G.ptr. */
+static int enqueue_ops(uint32_t images)
+{
+    const uint8_t *A = G.arena;
+    for (uint32_t i = 0; i < G.h.no; i++) {
+        const Op *o = G.ops + i;
+        const Tensor *a = G.ts + o->a, *b = G.ts + o->b, *z = G.ts + o->out;
+        void *zp = G.ptr[o->out];
+        const void *ap = G.ptr[o->a], *bp = G.ptr[o->b];
+        int rc = 0;
+        if (G.profile_enabled && (rc = uqk_record(i))) return rc;
+        switch (o->code) {
+        case 14: rc = uqk_conv(G.sp + i, ap, zp, images * a->d[0]); break;
+        case 15: rc = uqk_depthwise(G.sp + i, ap, zp, images * a->d[0]); break;
+        case 16: rc = uqk_pool(G.sp + i, ap, zp, images * a->d[0]); break;
+        case 18: {
+            const int32_t *q = (const int32_t *)(A + G.ts[o->p[0]].offset);
+            rc = uqk_add(ap, bp, zp, (uint64_t)images * z->bytes, G.dev_arena + G.ts[o->p[0]].offset + 8 * 4,
+                         q[0], q[1], q[2], q[3], q[4]);
+            break;
+        }
+        case 24: {
+            const int32_t *q = (const int32_t *)(A + b->offset);
+            rc = uqk_mean(ap, zp, images * a->d[0], (uint32_t)q[0], a->d[3], q[1], q[2], q[3], q[4]);
+            break;
+        }
+        case 5: rc = uqk_d2d(zp, ap, (size_t)images * z->bytes); break;
+        case 22: rc = uqk_lut(ap, zp, (uint64_t)images * a->bytes, bp, a->type == 3 ? 128u : 0u); break;
+        case 20: {
+            uint64_t outer = images, inner = 1;
+            uint32_t axis = o->p[0];
+            for (uint32_t d = 0; d < axis; d++) outer *= a->d[d];
+            for (uint32_t d = axis + 1; d < a->rank; d++) inner *= a->d[d];
+            size_t ac = (size_t)a->d[axis] * inner, bc = (size_t)b->d[axis] * inner;
+            rc = uqk_d2d_2d(zp, ac + bc, ap, ac, ac, outer);
+            if (!rc) rc = uqk_d2d_2d((uint8_t *)zp + ac, ac + bc, bp, bc, bc, outer);
+            break;
+        }
+        case 21: rc = uqk_resize(ap, zp, images * a->d[0], a->d[1], a->d[2], z->d[1], z->d[2], a->d[3], bp); break;
+        case 23: {
+            const int32_t *q = (const int32_t *)(A + b->offset);
+            int32_t off[4] = {q[0], q[2], q[4], q[6]};
+            rc = uqk_window4(ap, zp, images, a->d, z->d, off, (int32_t)(int8_t)(int32_t)o->p[0]);
+            break;
+        }
+        case 26: {
+            uint32_t in[4] = {1, 1, 1, 1}, out[4] = {1, 1, 1, 1};
+            int32_t off[4] = {0, 0, 0, 0};
+            uint32_t lead = 4 - a->rank;
+            for (uint32_t d = 0; d < a->rank; d++) {
+                in[lead + d] = a->d[d];
+                out[lead + d] = z->d[d];
+                off[lead + d] = -(int32_t)o->p[d];
+            }
+            rc = uqk_window4(ap, zp, images, in, out, off, 0);
+            break;
+        }
+        case 19: {
+            const uint32_t *list = (const uint32_t *)(A + b->offset);
+            size_t off = 0;
+            for (uint32_t j = 0; j < b->bytes / 4 && !rc; j++) {
+                const Tensor *t = G.ts + list[j];
+                if (t->flags) {
+                    for (uint32_t k = 0; k < images && !rc; k++)
+                        rc = uqk_d2d((uint8_t *)zp + (size_t)k * z->bytes + off, G.ptr[list[j]], t->bytes);
+                } else
+                    rc = uqk_d2d_2d((uint8_t *)zp + off, z->bytes, G.ptr[list[j]], t->bytes, t->bytes, images);
+                off += t->bytes;
+            }
+            break;
+        }
+        default: rc = 19;
+        }
+        if (rc) return rc;
+    }
+    if (G.profile_enabled) return uqk_record(G.h.no);
+    return 0;
+}
+
+static void bind_pointers(const void *d_in, void *d_out)
+{
+    for (uint32_t t = 0; t < G.h.nt; t++)
+        G.ptr[t] = G.ts[t].flags ? G.dev_arena + G.ts[t].offset : G.act[t];
+    if (d_in) G.ptr[G.h.input] = (uint8_t *)d_in;
+    if (d_out && G.h.output != G.h.input && !G.ts[G.h.output].flags) G.ptr[G.h.output] = (uint8_t *)d_out;
+}
+
+/* Copy the output tensor to a caller buffer when it was not produced there. */
+static int deliver_output_device(void *d_out, uint32_t images)
+{
+    const Tensor *t = G.ts + G.h.output;
+    if (G.ptr[G.h.output] == (uint8_t *)d_out) return 0;
+    if (t->flags) {
+        for (uint32_t k = 0; k < images; k++)
+            if (uqk_d2d((uint8_t *)d_out + (size_t)k * t->bytes, G.ptr[G.h.output], t->bytes)) return 24;
+        return 0;
+    }
+    return uqk_d2d(d_out, G.ptr[G.h.output], (size_t)images * t->bytes) ? 24 : 0;
+}
+
+static int finish_profile(void)
+{
+    if (!G.profile_enabled) return 0;
+    if (uqk_sync()) return 24;
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < G.h.no; i++) {
+        uint64_t ns = 0;
+        if (uqk_elapsed_ns(i, i + 1, &ns)) return 24;
+        G.ticks[2 + i] += ns;
+        total += ns;
+    }
+    G.ticks[0]++;
+    G.ticks[1] += total;
+    return 0;
+}
+
+static int fail(int rc)
+{
+    G.ready = 0;
+    return rc;
+}
+
+int ug_run_batch(const void *input, uint64_t ni, void *output, uint64_t no, uint32_t images)
+{
+    if (!G.ready || !input || !output || !images || ni != (uint64_t)images * ug_input_bytes() ||
+        no != (uint64_t)images * ug_output_bytes())
+        return 22;
+    if (ensure_capacity(images)) return fail(24);
+    bind_pointers(NULL, NULL);
+    if (uqk_h2d(G.ptr[G.h.input], input, ni)) return fail(24);
+    if (enqueue_ops(images)) return fail(24);
+    const Tensor *t = G.ts + G.h.output;
+    if (t->flags) {
+        if (uqk_sync()) return fail(24);
+        for (uint32_t k = 0; k < images; k++) memcpy((uint8_t *)output + (size_t)k * t->bytes, G.arena + t->offset, t->bytes);
+    } else {
+        if (uqk_d2h(output, G.ptr[G.h.output], no)) return fail(24);
+        if (uqk_sync()) return fail(24);
+    }
+    G.last_images = images;
+    return finish_profile() ? fail(24) : 0;
+}
+
+int ug_run(const void *input, uint32_t ni, void *output, uint32_t no)
+{
+    if (!G.ready || !input || !output || ni != ug_input_bytes() || no != ug_output_bytes()) return 22;
+    return ug_run_batch(input, ni, output, no, 1);
+}
+
+int ug_enqueue_device(const void *d_input, void *d_output, uint32_t images)
+{
+    if (!G.ready || !d_input || !d_output || !images) return 22;
+    if (ensure_capacity(images)) return fail(24);
+    bind_pointers(d_input, d_output);
+    if (enqueue_ops(images)) return fail(24);
+    if (deliver_output_device(d_output, images)) return fail(24);
+    G.last_images = images;
+    return 0;
+}
+
+int ug_synchronize(void)
+{
+    if (uqk_sync()) return fail(24);
+    return finish_profile() ? fail(24) : 0;
+}
+
+int ug_run_device(const void *d_input, void *d_output, uint32_t images)
+{
+    int rc = ug_enqueue_device(d_input, d_output, images);
+    if (rc) return rc;
+    return ug_synchronize();
+}
+
+int ug_snapshot_images(uint32_t index, void *out, uint64_t bytes)
+{
+    if (!G.ready || index >= G.h.nt || !out) return 22;
+    const Tensor *t = G.ts + index;
+    if (t->flags) {
+        if (bytes != t->bytes) return 22;
+        memcpy(out, G.arena + t->offset, t->bytes);
+        return 0;
+    }
+    if (!G.last_images || bytes != (uint64_t)G.last_images * t->bytes) return 22;
+    if (uqk_d2h(out, G.ptr[index], bytes) || uqk_sync()) return fail(24);
+    return 0;
+}
+
+int ug_snapshot(uint32_t index, void *out, uint32_t bytes)
+{
+    if (!G.ready || index >= G.h.nt || !out || bytes != G.ts[index].bytes) return 22;
+    const Tensor *t = G.ts + index;
+    if (t->flags) {
+        memcpy(out, G.arena + t->offset, bytes);
+        return 0;
+    }
+    if (!G.last_images) {
+        memcpy(out, G.arena + t->offset, bytes); /* arena contents before any run */
+        return 0;
+    }
+    if (uqk_d2h(out, G.ptr[index], bytes) || uqk_sync()) return fail(24);
+    return 0;
+}
+
+int ug_profile(uint32_t command, void *out, uint32_t bytes)
+{
+    if (!G.ready || command > 2 || !out || (bytes != sizeof(G.ticks) && !(G.h.no <= 128 && bytes == 130 * 8))) return 22;
+    if (command == 1) memset(G.ticks, 0, sizeof G.ticks);
+    if (command < 2) G.profile_enabled = (int)command;
+    memcpy(out, G.ticks, bytes);
+    return 0;
+}
+
+int ug_stream_begin(void)
+{
+    if (G.stream_active) return 24;
+    if (!G.ready) return 22;
+    if (G.vision_only && G.h.reserved) G.stream_active = 1;
+    return 0;
+}
+
+int ug_stream_end(void)
+{
+    if (!G.stream_active) return 0;
+    G.stream_active = 0;
+    return 0;
+}
+
+void *ug_device_alloc(uint64_t bytes)
+{
+    if (uqk_init()) return NULL;
+    return uqk_malloc((size_t)bytes);
+}
+
+int ug_device_free(void *d)
+{
+    uqk_free(d);
+    return 0;
+}
+
+int ug_device_upload(void *d_dst, const void *src, uint64_t bytes)
+{
+    if (uqk_init() || uqk_h2d(d_dst, src, (size_t)bytes) || uqk_sync()) return 24;
+    return 0;
+}
+
+int ug_device_download(void *dst, const void *d_src, uint64_t bytes)
+{
+    if (uqk_init() || uqk_d2h(dst, d_src, (size_t)bytes) || uqk_sync()) return 24;
+    return 0;
+}

@@ -1,0 +1,69 @@
+/* Thin C ABI between the plain-C graph host (graph.c) and the gfx950 HIP
+ * kernels (kernels.hip). Plain pointers and integers only: device pointers
+ * are opaque `void *` on the host side. Every launcher enqueues on the
+ * library's single HIP stream and returns 0 or a HIP error code. */
+#ifndef UQK_H
+#define UQK_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Spatial op descriptor shared by conv (code 14), depthwise (15) and pool (16).
+ * Geometry is the qnn.c:12-16 parameter block; the device tables are built at
+ * load time by graph.c:
+ *   w    conv: [oc_pad][kpad] signed int8, k = (ky, kx, ic), zero beyond K
+ *        depthwise: [taps][C] signed int8 (the plan's own layout)
+ *   epi  int32 x4 per channel: corrected bias folded for signed inputs
+ *        (bias + 128*sum(w) [+ xz*tail weights]), multiplier, shift, 0
+ *   kmap conv gathers: int32 x4 per gather group {ky*dh, kx*dw, ic, 0}
+ *   lut  optional fused 256-entry post table (uq_post) */
+typedef struct {
+    int32_t ih, iw, ic, oh, ow, oc;
+    int32_t kh, kw, sh, sw, dh, dw, pt, pl;
+    int32_t xz, yz, lo, hi;
+    int32_t K, kpad, oc_pad, mode, nt, rb, is_max, vec;
+    const void *w;
+    const void *epi;
+    const void *kmap;
+    const void *lut;
+} UQKSpatial;
+
+enum { UQK_PW = 0, UQK_G16 = 1, UQK_G4 = 2, UQK_G1 = 3 };
+
+int uqk_init(void);
+int uqk_device_count(void);
+void *uqk_malloc(size_t bytes);
+void uqk_free(void *p);
+int uqk_h2d(void *dst, const void *src, size_t bytes);        /* async on the stream */
+int uqk_d2h(void *dst, const void *src, size_t bytes);        /* async on the stream */
+int uqk_d2d(void *dst, const void *src, size_t bytes);        /* async on the stream */
+int uqk_d2d_2d(void *dst, size_t dpitch, const void *src, size_t spitch, size_t width, size_t height);
+int uqk_sync(void);
+int uqk_last_error(void);
+
+int uqk_conv(const UQKSpatial *d, const void *x, void *y, uint32_t batches);
+int uqk_depthwise(const UQKSpatial *d, const void *x, void *y, uint32_t batches);
+int uqk_pool(const UQKSpatial *d, const void *x, void *y, uint32_t batches);
+int uqk_add(const void *a, const void *b, void *y, uint64_t count, const void *tables,
+            int32_t m, int32_t shift, int32_t yz, int32_t lo, int32_t hi);
+int uqk_mean(const void *x, void *y, uint32_t batches, uint32_t pixels, uint32_t channels,
+             int32_t xz, int32_t yz, int32_t m, int32_t shift);
+int uqk_lut(const void *x, void *y, uint64_t count, const void *table, uint32_t flip);
+int uqk_resize(const void *x, void *y, uint32_t batches, uint32_t ih, uint32_t iw, uint32_t oh, uint32_t ow,
+               uint32_t c, const void *offsets);
+/* 4-D NHWC-order gather used by pad (code 23) and slice (code 26), per image:
+ * out[i0,i1,i2,i3] = in[i0-o0, i1-o1, i2-o2, i3-o3] when inside `in`, else fill. */
+int uqk_window4(const void *x, void *y, uint32_t images, const uint32_t in_dims[4], const uint32_t out_dims[4],
+                const int32_t offset[4], int32_t fill);
+
+/* Timing: a pool of HIP events recorded on the library stream. */
+int uqk_events(uint32_t count);
+int uqk_record(uint32_t index);
+int uqk_elapsed_ns(uint32_t first, uint32_t second, uint64_t *ns);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,129 @@
+"""ctypes binding of libuq_hip.so, the C-ABI GPU library (include/uq_graph.h).
+
+Mirrors how the reference's own tests bind its native library
+(tests/test_residual_add.py:62-69: ug_load / ug_run through ctypes), plus the
+batch extension. Raises if the built library is missing: there is no CPU
+fallback anywhere in the product path.
+"""
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+DEFAULT_LIBRARY = HERE / "libuq_hip.so"
+
+# Every function declared in include/uq_graph.h: (name, restype, argtypes).
+SIGNATURES = [
+    ("ug_load", C.c_int, [C.c_void_p, C.c_uint32]),
+    ("ug_run", C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32]),
+    ("ug_input_bytes", C.c_uint32, []),
+    ("ug_output_bytes", C.c_uint32, []),
+    ("ug_snapshot", C.c_int, [C.c_uint32, C.c_void_p, C.c_uint32]),
+    ("ug_profile", C.c_int, [C.c_uint32, C.c_void_p, C.c_uint32]),
+    ("ug_stream_begin", C.c_int, []),
+    ("ug_stream_end", C.c_int, []),
+    ("ug_run_batch", C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64, C.c_uint32]),
+    ("ug_run_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32]),
+    ("ug_enqueue_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32]),
+    ("ug_synchronize", C.c_int, []),
+    ("ug_snapshot_images", C.c_int, [C.c_uint32, C.c_void_p, C.c_uint64]),
+    ("ug_device_alloc", C.c_void_p, [C.c_uint64]),
+    ("ug_device_free", C.c_int, [C.c_void_p]),
+    ("ug_device_upload", C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64]),
+    ("ug_device_download", C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64]),
+    ("ug_op_count", C.c_uint32, []),
+]
+
+
+class NativeError(RuntimeError):
+    def __init__(self, where, code):
+        super().__init__(f"{where} returned {code}")
+        self.code = code
+
+
+def open_library(path=None):
+    path = Path(path or os.environ.get("UQ_HIP_LIBRARY", DEFAULT_LIBRARY))
+    if not path.exists():
+        raise FileNotFoundError(f"{path} is not built; run __graft_entry__.build()")
+    lib = C.CDLL(str(path))
+    for name, res, args in SIGNATURES:
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+class Graph:
+    """One loaded plan in the (process-global) GPU library."""
+
+    def __init__(self, plan, lib=None):
+        self.lib = lib or open_library()
+        self.plan = bytes(plan)
+        self._buf = C.create_string_buffer(self.plan, len(self.plan))
+        rc = self.lib.ug_load(self._buf, len(self.plan))
+        if rc:
+            raise NativeError("ug_load", rc)
+        self.input_bytes = self.lib.ug_input_bytes()
+        self.output_bytes = self.lib.ug_output_bytes()
+
+    def run(self, x):
+        x = np.ascontiguousarray(x, dtype=np.int8).reshape(-1)
+        y = np.empty(self.output_bytes, np.int8)
+        rc = self.lib.ug_run(x.ctypes.data, x.nbytes, y.ctypes.data, y.nbytes)
+        if rc:
+            raise NativeError("ug_run", rc)
+        return y
+
+    def run_batch(self, x, images):
+        x = np.ascontiguousarray(x, dtype=np.int8).reshape(-1)
+        y = np.empty(images * self.output_bytes, np.int8)
+        rc = self.lib.ug_run_batch(x.ctypes.data, x.nbytes, y.ctypes.data, y.nbytes, images)
+        if rc:
+            raise NativeError("ug_run_batch", rc)
+        return y
+
+    def snapshot_images(self, tensor, nbytes):
+        y = np.empty(nbytes, np.int8)
+        rc = self.lib.ug_snapshot_images(tensor, y.ctypes.data, nbytes)
+        if rc:
+            raise NativeError("ug_snapshot_images", rc)
+        return y
+
+    def profile(self, command):
+        counters = np.zeros(514, np.uint64)
+        rc = self.lib.ug_profile(command, counters.ctypes.data, counters.nbytes)
+        if rc:
+            raise NativeError("ug_profile", rc)
+        return counters
+
+
+class DeviceBuffer:
+    """A device allocation made through the library's helpers."""
+
+    def __init__(self, lib, nbytes):
+        self.lib = lib
+        self.nbytes = int(nbytes)
+        self.ptr = lib.ug_device_alloc(self.nbytes)
+        if not self.ptr:
+            raise MemoryError(f"ug_device_alloc({nbytes}) failed")
+
+    def upload(self, array):
+        a = np.ascontiguousarray(array).reshape(-1).view(np.uint8)
+        assert a.nbytes <= self.nbytes
+        rc = self.lib.ug_device_upload(self.ptr, a.ctypes.data, a.nbytes)
+        if rc:
+            raise NativeError("ug_device_upload", rc)
+
+    def download(self, nbytes=None):
+        out = np.empty(self.nbytes if nbytes is None else nbytes, np.int8)
+        rc = self.lib.ug_device_download(out.ctypes.data, self.ptr, out.nbytes)
+        if rc:
+            raise NativeError("ug_device_download", rc)
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.lib.ug_device_free(self.ptr)
+            self.ptr = None

@@ -1,0 +1,122 @@
+"""The five seeded INT8 workloads, as batch-1 plans plus an image count.
+
+Every plan is a single-image plan in the reference's format (the reference
+loader caps one plan at a 16 MiB arena and 2e9 MACs, graph.h:7-9); batches are
+run by stacking images on the leading dimension through the batch entry point.
+
+  pointwise   1x1 conv 56x56x32 -> 64, batch 1, xz -3, yz 5, ReLU6
+  dw3s1 / dw3s2 / dw5s1 / dw5s2
+              depthwise microbenchmarks, batch 64
+  mnv4        MobileNetV4-Conv-Small-shaped classifier, 224x224x3, batch 256
+              (the 60-op topology of models/mobilenetv4-small.uqmodel)
+  yolo        YOLO26n-shaped detector, 320x320x3, batch 64
+  head        1x1 7x7x960 -> 1280, batch 512 (M=25088, K=960, N=1280)
+  conv3x3     3x3 s1 80x80x128 -> 128, batch 512 (K=1152)
+"""
+import numpy as np
+
+from uq_plan import Plan, Rng
+
+# 6/ys for the ReLU6 clamp of the pointwise case; the scale is not given by
+# the workload description, so it is fixed here: ys = 0.05 -> q6 = 120.
+POINTWISE_Q6 = 120
+
+
+def pointwise(seed=0, tail_weights=False):
+    p = Plan(seed)
+    x = p.input((1, 56, 56, 32), zp=-3)
+    z = p.conv(x, 64, k=1, act="relu6", yz=5, q6=POINTWISE_Q6, w_sigma=40, bias_sigma=4096,
+               shift=(-10, -4), tail_weights=tail_weights)
+    return p.build(z), 1
+
+
+DW_CASES = {
+    "dw3s1": dict(hw=112, c=32, k=3, stride=1),
+    "dw3s2": dict(hw=112, c=64, k=3, stride=2),
+    "dw5s1": dict(hw=28, c=240, k=5, stride=1),
+    "dw5s2": dict(hw=56, c=96, k=5, stride=2),
+}
+
+
+def depthwise(case, seed=1, images=64):
+    spec = DW_CASES[case]
+    p = Plan(seed * 100 + list(DW_CASES).index(case))
+    x = p.input((1, spec["hw"], spec["hw"], spec["c"]), zp=int(Rng(seed, 5).integers(1, -128, 127)[0]))
+    z = p.depthwise(x, k=spec["k"], stride=spec["stride"], act="relu6", yz=-20, q6=110,
+                    w_sigma=40, bias_sigma=2048, shift=(-10, -4))
+    return p.build(z), images
+
+
+def mnv4(seed=2, images=256, calibrate=True):
+    """MobileNetV4-Conv-Small-shaped network: stem, fused-IB stages, UIB blocks
+    with 3x3/5x5 depthwise, residual adds, global mean, 1x1 head to 1280 and a
+    1000-way classifier; same op sequence and shapes as the reference's bundled
+    plan, with seeded random constants."""
+    p = Plan(seed, threads=2)
+    c = dict(calibrate=calibrate)
+    x = p.input((1, 224, 224, 3), zp=-13)
+    t = p.conv(x, 32, k=3, stride=2, act="relu", yz=-128, **c)            # stem
+    t = p.conv(t, 32, k=3, stride=2, act="relu", yz=-128, **c)            # fused IB
+    t = p.conv(t, 32, k=1, act="none", **c)
+    t = p.conv(t, 96, k=3, stride=2, act="relu", yz=-128, **c)
+    t = p.conv(t, 64, k=1, act="none", **c)
+    t = p.depthwise(t, k=5, act="none", **c)                               # UIB ExtraDW
+    t = p.conv(t, 192, k=1, act="relu", yz=-128, **c)
+    t = p.depthwise(t, k=5, stride=2, act="relu", yz=-128, **c)
+    x1 = p.conv(t, 96, k=1, act="none", **c)
+    for _ in range(4):                                                     # UIB IB, 14x14
+        t = p.conv(x1, 192, k=1, act="relu", yz=-128, **c)
+        t = p.depthwise(t, k=3, act="relu", yz=-128, **c)
+        t = p.conv(t, 96, k=1, act="none", **c)
+        x1 = p.add(t, x1)
+    t = p.depthwise(x1, k=3, act="none", **c)                              # UIB ConvNext
+    t = p.conv(t, 384, k=1, act="relu", yz=-128, **c)
+    t = p.conv(t, 96, k=1, act="none", **c)
+    x1 = p.add(t, x1)
+    t = p.depthwise(x1, k=3, act="none", **c)                              # UIB ExtraDW s2
+    t = p.conv(t, 576, k=1, act="relu", yz=-128, **c)
+    t = p.depthwise(t, k=3, stride=2, act="relu", yz=-128, **c)
+    y = p.conv(t, 128, k=1, act="none", **c)
+    t = p.depthwise(y, k=5, act="none", **c)                               # UIB ExtraDW 7x7
+    t = p.conv(t, 512, k=1, act="relu", yz=-128, **c)
+    t = p.depthwise(t, k=5, act="relu", yz=-128, **c)
+    t = p.conv(t, 128, k=1, act="none", **c)
+    y = p.add(t, y)
+    for expand, k in ((512, 5), (384, 5), (512, 3), (512, 3)):             # UIB IB 7x7
+        t = p.conv(y, expand, k=1, act="relu", yz=-128, **c)
+        t = p.depthwise(t, k=k, act="relu", yz=-128, **c)
+        t = p.conv(t, 128, k=1, act="none", **c)
+        y = p.add(t, y)
+    t = p.conv(y, 960, k=1, act="relu", yz=-128, **c)
+    t = p.mean(t)
+    t = p.conv(t, 1280, k=1, act="relu", yz=-128, **c)
+    t = p.copy(t)
+    t = p.conv(t, 1000, k=1, act="none", **c)
+    t = p.copy(t, (1, 1000))
+    return p.build(t), images
+
+
+def head(seed=4, images=512):
+    p = Plan(seed)
+    x = p.input((1, 7, 7, 960), zp=-7)
+    z = p.conv(x, 1280, k=1, act="relu6", yz=-100, q6=120, w_sigma=40, bias_sigma=4096, calibrate=True)
+    return p.build(z), images
+
+
+def conv3x3(seed=5, images=512):
+    p = Plan(seed)
+    x = p.input((1, 80, 80, 128), zp=9)
+    z = p.conv(x, 128, k=3, stride=1, act="relu6", yz=-100, q6=120, w_sigma=40, bias_sigma=4096, calibrate=True)
+    return p.build(z), images
+
+
+WORKLOADS = {
+    "pointwise": pointwise,
+    "dw3s1": lambda **kw: depthwise("dw3s1", **kw),
+    "dw3s2": lambda **kw: depthwise("dw3s2", **kw),
+    "dw5s1": lambda **kw: depthwise("dw5s1", **kw),
+    "dw5s2": lambda **kw: depthwise("dw5s2", **kw),
+    "mnv4": mnv4,
+    "head": head,
+    "conv3x3": conv3x3,
+}
