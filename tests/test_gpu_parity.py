@@ -84,10 +84,15 @@ def test_snapshot_intermediate(lib):
     g = Graph(plan, lib)
     g.run_batch(x, images)
     recs = P.tensor_records(plan)
-    for t in (3, 40, 120):
+    activations = [t for t, r in enumerate(recs) if not r[8]]
+    consts = [t for t, r in enumerate(recs) if r[8]]
+    for t in (activations[1], activations[len(activations) // 2], activations[-2]):
         nbytes = images * recs[t][1]
         _, want = oracle_run(plan, x, images, P.output_bytes(plan), snap=t, snap_bytes=nbytes)
         _assert_same(g.snapshot_images(t, nbytes), want, f"snapshot tensor {t}")
+    t = consts[3]
+    _, want = oracle_run(plan, x, images, P.output_bytes(plan), snap=t, snap_bytes=recs[t][1])
+    _assert_same(g.snapshot_images(t, recs[t][1]), want, f"snapshot constant {t}")
 
 
 def test_profile_counters(lib):
