@@ -458,10 +458,13 @@ static void release_device(void)
 
 static uint32_t round_up(uint32_t v, uint32_t m) { return (v + m - 1) / m * m; }
 
-/* N tile count per block (16 channels each): the least padded choice. */
-static int choose_nt(int oc)
+/* N tile count per block (16 channels each): the least padded choice, or the
+ * narrowest when each image has only a few output rows (FC-shaped layers,
+ * where channel slices are the only source of parallelism). */
+static int choose_nt(int oc, uint64_t rows_per_image)
 {
     static const int opts[4] = {8, 6, 4, 2};
+    if (rows_per_image <= 4) return 2;
     int best = 8, waste = 1 << 30;
     for (int i = 0; i < 4; i++) {
         int bn = 16 * opts[i], pad = (oc + bn - 1) / bn * bn - oc;
@@ -474,6 +477,53 @@ typedef struct { size_t w, epi, kmap, end; } Layout;
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+/* Kernel configuration of one conv (code 14): K padding, channel tile, and
+ * the A-operand source. Spatial convs stage their input rows in LDS when the
+ * tile fits in 64 KiB; otherwise lanes gather straight from HBM. */
+typedef struct { int K, kpad, nt, oc_pad, mode, table_bytes, icp; } ConvPlan;
+
+static ConvPlan conv_plan(const Op *o)
+{
+    const int32_t *q = (const int32_t *)(G.arena + G.ts[o->p[0]].offset);
+    const Tensor *z = G.ts + o->out;
+    ConvPlan c;
+    int ic = q[16], oc = q[17];
+    c.K = q[0] * q[1] * ic;
+    c.icp = ic;
+    c.kpad = (int)round_up((uint32_t)c.K, 64);
+    c.nt = choose_nt(oc, (uint64_t)z->d[0] * z->d[1] * z->d[2]);
+    c.oc_pad = (int)round_up((uint32_t)oc, (uint32_t)(16 * c.nt));
+    int pointwise = q[0] == 1 && q[1] == 1 && q[2] == 1 && q[3] == 1 && !q[6] && !q[7] && !q[8] && !q[9];
+    if (pointwise && ic % 16 == 0) {
+        c.mode = UQK_PW;
+        c.table_bytes = 16;
+        return c;
+    }
+    /* Row-staged modes: 16-byte K slices when IC % 16 == 0, otherwise taps
+     * of icp = roundup(IC, 4) bytes (zero weights on the padded channels). */
+    int icp = ic % 16 == 0 ? ic : (ic + 3) & ~3;
+    int kw4 = q[0] * q[1] * icp;
+    int rows_mode = ic % 16 == 0 ? UQK_ROWS16 : kw4 <= UQ_MAX_K ? UQK_ROWS4 : -1;
+    if (rows_mode >= 0) {
+        UQKSpatial t;
+        memset(&t, 0, sizeof t);
+        t.ow = q[11]; t.sw = q[3]; t.kh = q[0]; t.kw = q[1]; t.sh = q[2]; t.dh = q[4]; t.dw = q[5];
+        t.ic = ic; t.K = kw4; t.nt = c.nt; t.mode = rows_mode;
+        if (uqk_conv_rows_lds(&t, 2) <= 65536) {
+            c.mode = rows_mode;
+            c.icp = icp;
+            c.K = kw4;
+            c.kpad = (int)round_up((uint32_t)kw4, 64);
+            c.table_bytes = (rows_mode == UQK_ROWS16 ? c.K / 16 : c.K / 4) * 4 + 16;
+            return c;
+        }
+    }
+    int group = ic % 16 == 0 ? 16 : ic % 4 == 0 ? 4 : 1;
+    c.mode = group == 16 ? UQK_G16 : group == 4 ? UQK_G4 : UQK_G1;
+    c.table_bytes = (c.K / group + 1) * 16;
+    return c;
+}
+
 /* Sizes of one spatial op's prepared tables in the device pool. */
 static Layout spatial_layout(const Op *o, size_t at)
 {
@@ -481,18 +531,42 @@ static Layout spatial_layout(const Op *o, size_t at)
     Layout L = {at, at, at, at};
     int oc = q[17];
     if (o->code == 14) {
-        int K = q[0] * q[1] * q[16], kpad = (int)round_up((uint32_t)K, 64), nt = choose_nt(oc);
-        int oc_pad = (int)round_up((uint32_t)oc, (uint32_t)(16 * nt));
-        int ic = q[16], group = ic % 16 == 0 ? 16 : ic % 4 == 0 ? 4 : 1;
+        ConvPlan c = conv_plan(o);
         L.w = at;
-        L.epi = align256(L.w + (size_t)oc_pad * kpad);
-        L.kmap = align256(L.epi + (size_t)oc * 16);
-        L.end = align256(L.kmap + (size_t)(K / group + 1) * 16);
+        L.epi = align256(L.w + (size_t)c.oc_pad * c.kpad);
+        L.kmap = align256(L.epi + (size_t)oc * 32);
+        L.end = align256(L.kmap + (size_t)c.table_bytes);
     } else if (o->code == 15) {
+        int groups = (q[0] * q[1] + 3) / 4;
         L.epi = at;
-        L.end = align256(L.epi + (size_t)oc * 16);
+        L.w = align256(L.epi + (size_t)oc * 32);
+        L.end = align256(L.w + (size_t)groups * oc * 4);
     }
     return L;
+}
+
+/* Per-channel epilogue record (32 bytes) for the single 64-bit multiply-add
+ * form of requantisation used by the kernels. With v = acc + bias (int32,
+ * exact by the load-time bound proof), n = max(-shift, 0), T = 31 + n:
+ *   scale(v, m, shift) = ((v << max(shift, 0)) * m + c1 - corr) >> T
+ *   c1   = 2^30 + (n ? 2^(30+n) : 0)
+ *   corr = 2^31 when n > 0 and (v << ls) * m < -2^30, i.e. q < cthr = 2^(30+n)
+ * The first rounding (v*m + 2^30) >> 31 and the ties-away rounding shift of
+ * qnn.c:61-83 collapse into one floor because floor(floor(x/a)+b)/c) =
+ * floor((x + a*b)/(a*c)) for integer b; the correction turns round-half-up
+ * into ties-away for negative intermediates (the same identity the
+ * reference's signed affine path relies on, qnn.c:284-296). */
+static void epilogue_record(int32_t *e, int64_t bias, int32_t m, int32_t shift)
+{
+    int n = shift < 0 ? -shift : 0;
+    int64_t c1 = ((int64_t)1 << 30) + (n ? ((int64_t)1 << (30 + n)) : 0);
+    int64_t cthr = n ? ((int64_t)1 << (30 + n)) : INT64_MIN;
+    e[0] = (int32_t)(uint32_t)(uint64_t)bias;
+    e[1] = m;
+    e[2] = shift > 0 ? shift : 0;
+    e[3] = 31 + n;
+    memcpy(e + 4, &c1, 8);
+    memcpy(e + 6, &cthr, 8);
 }
 
 /* Build one spatial op's descriptor and host-side tables (graph-time work of
@@ -509,6 +583,7 @@ static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
     d->kh = q[0]; d->kw = q[1]; d->sh = q[2]; d->sw = q[3]; d->dh = q[4]; d->dw = q[5];
     d->pt = q[6]; d->pl = q[7];
     d->xz = q[12]; d->yz = q[13]; d->lo = q[14]; d->hi = q[15];
+    d->corr = q[14] < q[13];
     d->is_max = o->code == 16 ? q[19] : 0;
     d->vec = d->oc % 16 == 0 ? 16 : d->oc % 4 == 0 ? 4 : 1;
     if (o->code != 16 && o->p[1]) d->lut = G.dev_arena + G.ts[o->p[1] - 1].offset;
@@ -516,12 +591,10 @@ static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
     const int32_t *bias = q + UQ_HEAD, *mult = bias + oc, *shift = mult + oc;
     const int8_t *w = (const int8_t *)(G.arena + G.ts[o->b].offset);
     if (o->code == 14) {
-        int K = q[0] * q[1] * q[16], kp = q[18], kpad = (int)round_up((uint32_t)K, 64), nt = choose_nt(oc);
-        int oc_pad = (int)round_up((uint32_t)oc, (uint32_t)(16 * nt)), ic = q[16];
-        int pointwise = q[0] == 1 && q[1] == 1 && q[2] == 1 && q[3] == 1 && !q[6] && !q[7] && !q[8] && !q[9];
-        int group = ic % 16 == 0 ? 16 : ic % 4 == 0 ? 4 : 1;
-        d->K = K; d->kpad = kpad; d->oc_pad = oc_pad; d->nt = nt; d->rb = 2;
-        d->mode = pointwise && group == 16 ? UQK_PW : group == 16 ? UQK_G16 : group == 4 ? UQK_G4 : UQK_G1;
+        ConvPlan cp = conv_plan(o);
+        int K = cp.K, kp = q[18], kpad = cp.kpad, oc_pad = cp.oc_pad, ic = q[16], icp = cp.icp;
+        int Klog = q[0] * q[1] * ic;
+        d->K = K; d->kpad = kpad; d->oc_pad = oc_pad; d->nt = cp.nt; d->rb = 2; d->mode = cp.mode;
         int8_t *wt = (int8_t *)host_pool + L->w;
         int32_t *epi = (int32_t *)(host_pool + L->epi);
         int32_t *kmap = (int32_t *)(host_pool + L->kmap);
@@ -531,38 +604,51 @@ static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
             for (int k = 0; k < kp; k++) {
                 int v = packed_weight(w, (uint32_t)n, (uint32_t)k, (uint32_t)kp);
                 all += v;
-                if (k < K) wt[(size_t)n * kpad + k] = (int8_t)v;
+                /* Logical k = (tap, c) lands at tap * icp + c of the device row. */
+                if (k < Klog) wt[(size_t)n * kpad + (k / ic) * icp + k % ic] = (int8_t)v;
                 else tail += v;
             }
             /* u = s + 128 on every column; the K tail holds xz + 128. */
             int64_t b2 = (int64_t)bias[n] + 128 * all + (int64_t)q[12] * tail;
-            epi[4 * n + 0] = (int32_t)(uint32_t)(uint64_t)b2;
-            epi[4 * n + 1] = mult[n];
-            epi[4 * n + 2] = shift[n];
-            epi[4 * n + 3] = 0;
+            epilogue_record(epi + 8 * n, b2, mult[n], shift[n]);
         }
-        for (int g = 0; g < K / group; g++) {
-            int k = g * group, t = k / ic, c = k % ic, ky = t / q[1], kx = t % q[1];
-            kmap[4 * g + 0] = ky * q[4];
-            kmap[4 * g + 1] = kx * q[5];
-            kmap[4 * g + 2] = c;
-            kmap[4 * g + 3] = 0;
+        if (cp.mode == UQK_ROWS16 || cp.mode == UQK_ROWS4) {
+            /* Slice -> byte offset inside the LDS row tile (full-width rows,
+             * icp bytes per staged pixel). */
+            int step = cp.mode == UQK_ROWS16 ? 16 : 4;
+            int cols = (q[11] - 1) * q[3] + (q[1] - 1) * q[5] + 1;
+            for (int g = 0; g < K / step; g++) {
+                int k = g * step, t = k / icp, c = k % icp, ky = t / q[1], kx = t % q[1];
+                kmap[g] = ((ky * q[4]) * cols + kx * q[5]) * icp + c;
+            }
+        } else if (cp.mode != UQK_PW) {
+            int group = cp.mode == UQK_G16 ? 16 : cp.mode == UQK_G4 ? 4 : 1;
+            for (int g = 0; g < K / group; g++) {
+                int k = g * group, t = k / ic, c = k % ic, ky = t / q[1], kx = t % q[1];
+                kmap[4 * g + 0] = ky * q[4];
+                kmap[4 * g + 1] = kx * q[5];
+                kmap[4 * g + 2] = c;
+                kmap[4 * g + 3] = 0;
+            }
         }
         d->w = G.dev_prep + L->w;
         d->epi = G.dev_prep + L->epi;
         d->kmap = G.dev_prep + L->kmap;
     } else if (o->code == 15) {
-        int taps = q[0] * q[1];
+        int taps = q[0] * q[1], groups = (taps + 3) / 4;
         int32_t *epi = (int32_t *)(host_pool + L->epi);
+        int8_t *wd = (int8_t *)host_pool + L->w;
         for (int c = 0; c < oc; c++) {
             int64_t all = 0;
             for (int t = 0; t < taps; t++) all += w[t * oc + c];
-            epi[4 * c + 0] = (int32_t)(uint32_t)(uint64_t)((int64_t)bias[c] + 128 * all);
-            epi[4 * c + 1] = mult[c];
-            epi[4 * c + 2] = shift[c];
-            epi[4 * c + 3] = 0;
+            epilogue_record(epi + 8 * c, (int64_t)bias[c] + 128 * all, mult[c], shift[c]);
+            /* Four consecutive taps of one channel per 32-bit word, for dot4. */
+            for (int g = 0; g < groups; g++)
+                for (int j = 0; j < 4; j++)
+                    wd[((size_t)g * oc + c) * 4 + j] = 4 * g + j < taps ? w[(4 * g + j) * oc + c] : 0;
         }
         d->w = G.dev_arena + G.ts[o->b].offset;
+        d->wdot = G.dev_prep + L->w;
         d->epi = G.dev_prep + L->epi;
     }
 }
@@ -671,7 +757,12 @@ static int enqueue_ops(uint32_t images)
             rc = uqk_mean(ap, zp, images * a->d[0], (uint32_t)q[0], a->d[3], q[1], q[2], q[3], q[4]);
             break;
         }
-        case 5: rc = uqk_d2d(zp, ap, (size_t)images * z->bytes); break;
+        case 5:
+            /* Every tensor is written once (graph.c:72 forbids redefinition),
+             * so an internal copy can alias its source instead of moving bytes. */
+            if (G.ptr[o->out] == G.act[o->out]) G.ptr[o->out] = (uint8_t *)G.ptr[o->a];
+            else rc = uqk_d2d(zp, ap, (size_t)images * z->bytes);
+            break;
         case 22: rc = uqk_lut(ap, zp, (uint64_t)images * a->bytes, bp, a->type == 3 ? 128u : 0u); break;
         case 20: {
             uint64_t outer = images, inner = 1;

@@ -50,26 +50,56 @@ __device__ __forceinline__ int uq_scale(int v, int m, int s)
     return base + (rem > ((mask >> 1) + (unsigned)(h < 0)) ? 1 : 0);
 }
 
-__device__ __forceinline__ int uq_requant(int acc, int bias, int m, int s, int yz, int lo, int hi)
-{
-    int v = (int)((unsigned)acc + (unsigned)bias);
-    v = uq_scale(v, m, s) + yz;
-    return min(max(v, lo), hi);
-}
 
 __device__ __forceinline__ int sbyte(int word, int b) { return (int)(signed char)(word >> (8 * b)); }
+
+// Per-channel constants of the one-multiply requantisation (layout and
+// derivation at epilogue_record in graph.c): exact for every shift in
+// [-31, 15]; `corr` enables the ties-away correction for layers whose clamp
+// can let negative rounded values through (act_min < output zero point).
+struct Epi {
+    int bias, m, ls, T;
+    long long c1, cthr;
+};
+
+__device__ __forceinline__ Epi load_epi(const int4 *epi, int c)
+{
+    const int4 a = epi[2 * c], b = epi[2 * c + 1];
+    Epi e;
+    e.bias = a.x; e.m = a.y; e.ls = a.z; e.T = a.w;
+    e.c1 = (long long)(((unsigned long long)(unsigned)b.y << 32) | (unsigned)b.x);
+    e.cthr = (long long)(((unsigned long long)(unsigned)b.w << 32) | (unsigned)b.z);
+    return e;
+}
+
+__device__ __forceinline__ int uq_requant_affine(int acc, const Epi &e, int corr, int yz, int lo, int hi)
+{
+    const int v = (int)(((unsigned)acc + (unsigned)e.bias) << e.ls);
+    long long q = (long long)v * (long long)e.m + e.c1;
+    if (corr && q < e.cthr) q -= (1LL << 31);
+    const int r = (int)(q >> e.T);
+    return min(max(r + yz, lo), hi);
+}
 
 // ---------------------------------------------------------------------------
 // Implicit-GEMM convolution on v_mfma_i32_16x16x64_i8.
 //
 // A block is 4 waves; each wave owns RB x 16 output rows (pixels) and all
-// NT x 16 output channels of the block's channel slice. Each lane gathers one
-// 16-byte K slice of one row straight into the MFMA A operand (lane & 15 is
-// the row, lane >> 4 the K slice); the B operand is the matching 16-byte K
-// slice of the [oc_pad][kpad] weight matrix. A and B use the same lane -> K
-// assignment, so the sum is independent of the hardware's K order inside an
-// operand. The requantised bytes are staged in LDS and written as coalesced
-// 16-byte row segments.
+// NT x 16 output channels of the block's channel slice. Each lane supplies one
+// 16-byte K slice of one row as the MFMA A operand (lane & 15 is the row,
+// lane >> 4 the K slice); the B operand is the matching 16-byte K slice of the
+// [oc_pad][kpad] weight matrix. A and B use the same lane -> K assignment, so
+// the sum is independent of the hardware's K order inside an operand. The
+// next K step's operands are loaded before the current step's MFMAs issue.
+// The requantised bytes are staged in LDS and written as coalesced 16-byte
+// row segments.
+//
+// Two A sources:
+//   k_conv       pointwise rows read straight from HBM (MODE PW), or a
+//                per-lane gather through a k -> (dy, dx, c) table (G16/G4/G1)
+//   k_conv_rows  spatial convs: the block's input rows (with padding
+//                materialised as xz) are staged once in LDS, and every lane
+//                reads its K slices from there through a k -> LDS-offset table
 // ---------------------------------------------------------------------------
 struct ConvArgs {
     const int8_t *x;
@@ -77,8 +107,11 @@ struct ConvArgs {
     const int8_t *w;
     const int4 *epi;
     const int4 *kmap;
+    const int *delta;
     const uint8_t *lut;
-    int M, ih, iw, ic, oh, ow, oc, sh, sw, pt, pl, xz, yz, lo, hi, K, kpad, ohw;
+    long M;
+    int ih, iw, ic, icp, oh, ow, oc, kh, sh, sw, dh, pt, pl, xz, yz, lo, hi, K, kpad, ohw, corr;
+    int tiles, cols, rows_max;
 };
 
 template <int MODE>
@@ -129,18 +162,89 @@ __device__ __forceinline__ v4i gather16(const ConvArgs &a, const int8_t *base, i
     }
 }
 
-template <int RB, int NT, int MODE>
-__global__ __launch_bounds__(256) void k_conv(ConvArgs a)
+// Requantise a wave's RB*16 x NT*16 tile and store the valid rows
+// [row_base, row_limit). The MFMA result gives a lane one channel (lane & 15)
+// of four consecutive rows; the four bytes are packed into a word, and a 4x4
+// byte transpose across each quad of lanes (two DPP quad permutes, two
+// v_perm) turns that into one row x four channels per lane, stored as one
+// dword. Needs OC % 4 == 0 (so a quad's channels are all valid or all not);
+// other widths take byte stores.
+__device__ __forceinline__ int quad_transpose_bytes(int w, int lane)
+{
+    const int j = lane & 3;
+    const int x = __builtin_amdgcn_mov_dpp(w, 0x4E, 0xF, 0xF, true);        // quad_perm [2,3,0,1]
+    const int u = (int)__builtin_amdgcn_perm((unsigned)x, (unsigned)w, j < 2 ? 0x05040100u : 0x03020706u);
+    const int y = __builtin_amdgcn_mov_dpp(u, 0xB1, 0xF, 0xF, true);        // quad_perm [1,0,3,2]
+    return (int)__builtin_amdgcn_perm((unsigned)y, (unsigned)u, (j & 1) ? 0x03070105u : 0x06020400u);
+}
+
+__device__ __forceinline__ int pack4(int v0, int v1, int v2, int v3)
+{
+    const unsigned lo = __builtin_amdgcn_perm((unsigned)v1, (unsigned)v0, 0x0c0c0400u);
+    const unsigned hi = __builtin_amdgcn_perm((unsigned)v3, (unsigned)v2, 0x04000c0cu);
+    return (int)(lo | hi);
+}
+
+template <int RB, int NT>
+__device__ __forceinline__ void conv_store(const ConvArgs &a, const v4i (&acc)[RB][NT], int8_t *stage, int n0, int lane,
+                                           long row_base, long row_limit)
 {
     constexpr int R = RB * 16;
     constexpr int BN = NT * 16;
     constexpr int STRIDE = BN + 16;
+    const int lr = lane & 15, lg = lane >> 4;
+    const bool words = (a.oc & 3) == 0;
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int col = n0 + nt * 16 + lr;
+        const Epi e = load_epi(a.epi, col < a.oc ? col : 0);
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+            int v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[i] = uq_requant_affine(acc[rb][nt][i], e, a.corr, a.yz, a.lo, a.hi);
+                if (a.lut) v[i] = (int)(signed char)a.lut[v[i] + 128];
+            }
+            if (words) {
+                const int t = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
+                *(int *)(stage + (rb * 16 + lg * 4 + (lane & 3)) * STRIDE + nt * 16 + (lr & ~3)) = t;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) stage[(rb * 16 + lg * 4 + i) * STRIDE + nt * 16 + lr] = (int8_t)v[i];
+            }
+        }
+    }
+    __syncthreads();
+    const int ncols = min(BN, a.oc - n0);
+    if ((a.oc & 15) == 0) {
+        const int cpr = ncols >> 4;
+        for (int c = lane; c < R * cpr; c += 64) {
+            const int r = c / cpr, cc = c - r * cpr;
+            const long row = row_base + r;
+            if (row < row_limit)
+                *(v4i *)(a.y + row * a.oc + n0 + cc * 16) = *(const v4i *)(&stage[r * STRIDE + cc * 16]);
+        }
+    } else {
+        for (int c = lane; c < R * ncols; c += 64) {
+            const int r = c / ncols, cc = c - r * ncols;
+            const long row = row_base + r;
+            if (row < row_limit) a.y[row * a.oc + n0 + cc] = stage[r * STRIDE + cc];
+        }
+    }
+}
+
+template <int RB, int NT, int MODE>
+__global__ __launch_bounds__(256) void k_conv(ConvArgs a)
+{
+    constexpr int R = RB * 16;
+    constexpr int STRIDE = NT * 16 + 16;
     __shared__ __attribute__((aligned(16))) int8_t stage[4][R * STRIDE];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;
-    const int row0 = (blockIdx.x * 4 + wave) * R;
-    const int n0 = blockIdx.y * BN;
+    const long row0 = ((long)blockIdx.x * 4 + wave) * R;
+    const int n0 = blockIdx.y * NT * 16;
     const int xzw = (a.xz & 0xff) * 0x01010101;
 
     const int8_t *base[RB];
@@ -148,18 +252,19 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
     bool valid[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
-        const int row = row0 + rb * 16 + lr;
+        const long row = row0 + rb * 16 + lr;
         valid[rb] = row < a.M;
-        const int r = valid[rb] ? row : 0;
+        const long r = valid[rb] ? row : 0;
         if (MODE == UQK_PW) {
-            base[rb] = a.x + (long)r * a.ic;
+            base[rb] = a.x + r * a.ic;
             iy0[rb] = ix0[rb] = 0;
         } else {
-            const int n = r / a.ohw, rem = r - n * a.ohw;
+            const long n = r / a.ohw;
+            const int rem = (int)(r - n * a.ohw);
             const int oy = rem / a.ow, ox = rem - oy * a.ow;
             iy0[rb] = oy * a.sh - a.pt;
             ix0[rb] = ox * a.sw - a.pl;
-            base[rb] = a.x + (long)n * a.ih * a.iw * a.ic;
+            base[rb] = a.x + n * a.ih * a.iw * a.ic;
         }
     }
 
@@ -170,64 +275,220 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
         for (int nt = 0; nt < NT; nt++) acc[rb][nt] = (v4i){0, 0, 0, 0};
 
     const int8_t *wrow = a.w + (long)(n0 + lr) * a.kpad + lg * 16;
-    for (int k0 = 0; k0 < a.kpad; k0 += 64) {
-        const int kg = k0 + lg * 16;
-        v4i A[RB];
+    const int steps = a.kpad >> 6;
+    v4i A[RB], B[NT];
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++) A[rb] = gather16<MODE>(a, base[rb], iy0[rb], ix0[rb], valid[rb], kg, xzw);
+    for (int rb = 0; rb < RB; rb++) A[rb] = gather16<MODE>(a, base[rb], iy0[rb], ix0[rb], valid[rb], lg * 16, xzw);
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const v4i B = *(const v4i *)(wrow + (long)nt * 16 * a.kpad + k0);
+    for (int nt = 0; nt < NT; nt++) B[nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad);
+    for (int s = 0; s < steps; s++) {
+        v4i An[RB], Bn[NT];
+        const bool more = s + 1 < steps;
+        if (more) {
+            const int k1 = (s + 1) * 64;
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) An[rb] = gather16<MODE>(a, base[rb], iy0[rb], ix0[rb], valid[rb], k1 + lg * 16, xzw);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) Bn[nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad + k1);
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
 #pragma unroll
             for (int rb = 0; rb < RB; rb++)
-                acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[rb], B, acc[rb][nt], 0, 0, 0);
+                acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[rb], B[nt], acc[rb][nt], 0, 0, 0);
+        if (more) {
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) A[rb] = An[rb];
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) B[nt] = Bn[nt];
         }
     }
+    conv_store<RB, NT>(a, acc, stage[wave], n0, lane, row0, a.M);
+}
 
-    // Epilogue: lane holds column (lane & 15) and rows 4*(lane >> 4) + i.
-#pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        const int col = n0 + nt * 16 + lr;
-        const int4 e = col < a.oc ? a.epi[col] : make_int4(0, 0, 0, 0);
-#pragma unroll
-        for (int rb = 0; rb < RB; rb++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                int v = uq_requant(acc[rb][nt][i], e.x, e.y, e.z, a.yz, a.lo, a.hi);
-                if (a.lut) v = (int)(signed char)a.lut[v + 128];
-                stage[wave][(rb * 16 + lg * 4 + i) * STRIDE + nt * 16 + lr] = (int8_t)v;
-            }
-    }
-    __syncthreads();
-    const int ncols = min(BN, a.oc - n0);
-    if ((a.oc & 15) == 0) {
-        const int cpr = ncols >> 4;
-        for (int c = lane; c < R * cpr; c += 64) {
-            const int r = c / cpr, cc = c - r * cpr;
-            const int row = row0 + r;
-            if (row < a.M)
-                *(v4i *)(a.y + (long)row * a.oc + n0 + cc * 16) = *(const v4i *)(&stage[wave][r * STRIDE + cc * 16]);
+// Spatial conv with the block's input rows staged in LDS. A block covers BM =
+// 4*RB*16 consecutive output pixels of one image (tiles never straddle
+// images); the staged region is the rows those pixels touch, full width, with
+// out-of-image positions written as xz so the K loop has no bounds checks.
+// WORDS: IC % 16 != 0. Each staged pixel holds icp = IC rounded up to four
+// bytes (the extra channels are zero, and so are their weights), K counts
+// icp-wide taps, and an A slice is four aligned 4-byte LDS reads.
+template <int RB, int NT, bool WORDS>
+__global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
+{
+    constexpr int R = RB * 16;
+    constexpr int BM = 4 * R;
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int tile = blockIdx.x % a.tiles;
+    const long n = blockIdx.x / a.tiles;
+    const int n0 = blockIdx.y * NT * 16;
+    const int p0 = tile * BM, pend = min(p0 + BM, a.ohw);
+    const int oy_a = p0 / a.ow, oy_b = (pend - 1) / a.ow;
+    const int rows = (oy_b - oy_a) * a.sh + (a.kh - 1) * a.dh + 1;
+    const int rowbytes = a.cols * a.icp;
+    const int tile_bytes = (a.rows_max * rowbytes + 15) & ~15;
+    const int ndelta = WORDS ? a.K >> 2 : a.K >> 4;
+    int8_t *xt = smem;
+    int *dl = (int *)(smem + tile_bytes);
+    constexpr int STRIDE = NT * 16 + 16;
+    int8_t *stage = smem + tile_bytes + ((ndelta * 4 + 15) & ~15) + wave * R * STRIDE;
+
+    const int iy_lo = oy_a * a.sh - a.pt;
+    const int8_t *xim = a.x + n * a.ih * a.iw * a.ic;
+    if (!WORDS) {
+        const int xzw = (a.xz & 0xff) * 0x01010101;
+        const int cpr = rowbytes >> 4;
+        for (int q = threadIdx.x; q < rows * cpr; q += 256) {
+            const int r = q / cpr, b = (q - r * cpr) << 4;
+            const int col = b / a.ic, c = b - col * a.ic;
+            const int iy = iy_lo + r, ix = col - a.pl;
+            v4i v = {xzw, xzw, xzw, xzw};
+            if (iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw) v = *(const v4i *)(xim + ((long)iy * a.iw + ix) * a.ic + c);
+            *(v4i *)(xt + r * rowbytes + b) = v;
         }
     } else {
-        for (int c = lane; c < R * ncols; c += 64) {
-            const int r = c / ncols, cc = c - r * ncols;
-            const int row = row0 + r;
-            if (row < a.M) a.y[(long)row * a.oc + n0 + cc] = stage[wave][r * STRIDE + cc];
+        // One staged row at a time (a block-uniform loop), one LDS word per
+        // thread and iteration: no division when a pixel is a single word.
+        const int wpp = a.icp >> 2, wpr = a.cols * wpp, xzb = a.xz & 0xff;
+        for (int r = 0; r < rows; r++) {
+            const int iy = iy_lo + r;
+            const bool rowin = iy >= 0 && iy < a.ih;
+            const int8_t *srow = xim + (long)(rowin ? iy : 0) * a.iw * a.ic;
+            int *drow = (int *)(xt + r * rowbytes);
+            for (int wi = threadIdx.x; wi < wpr; wi += 256) {
+                const int col = wpp == 1 ? wi : wi / wpp, cw = wi - col * wpp;
+                const int ix = col - a.pl;
+                const bool in = rowin && ix >= 0 && ix < a.iw;
+                const int8_t *src = srow + (long)(in ? ix : 0) * a.ic + cw * 4;
+                int word = 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int b = cw * 4 + j < a.ic ? (in ? (int)(uint8_t)src[j] : xzb) : 0;
+                    word |= b << (8 * j);
+                }
+                drow[wi] = word;
+            }
         }
     }
+    for (int i = threadIdx.x; i < ndelta; i += 256) dl[i] = a.delta[i];
+    __syncthreads();
+
+    int lbase[RB];
+    bool valid[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+        const int p = p0 + wave * R + rb * 16 + lr;
+        valid[rb] = p < pend;
+        const int pp = valid[rb] ? p : p0;
+        const int oy = pp / a.ow, ox = pp - oy * a.ow;
+        lbase[rb] = ((oy - oy_a) * a.sh * a.cols + ox * a.sw) * a.icp;
+    }
+
+    v4i acc[RB][NT];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[rb][nt] = (v4i){0, 0, 0, 0};
+
+    const int8_t *wrow = a.w + (long)(n0 + lr) * a.kpad + lg * 16;
+    const int steps = a.kpad >> 6;
+    v4i B[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) B[nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad);
+    for (int s = 0; s < steps; s++) {
+        const int kg = s * 64 + lg * 16;
+        v4i Bn[NT];
+        const bool more = s + 1 < steps;
+        if (more) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) Bn[nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad + (s + 1) * 64);
+        }
+        v4i A[RB];
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+            v4i v = {0, 0, 0, 0};
+            if (valid[rb] && kg < a.K) {
+                if (!WORDS) {
+                    v = *(const v4i *)(xt + lbase[rb] + dl[kg >> 4]);
+                } else {
+                    const int w0 = kg >> 2;
+                    int r4[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) r4[j] = w0 + j < ndelta ? *(const int *)(xt + lbase[rb] + dl[w0 + j]) : 0;
+                    v = (v4i){r4[0], r4[1], r4[2], r4[3]};
+                }
+            }
+            A[rb] = v;
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++)
+                acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[rb], B[nt], acc[rb][nt], 0, 0, 0);
+        if (more) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) B[nt] = Bn[nt];
+        }
+    }
+    const long img0 = n * a.ohw;
+    conv_store<RB, NT>(a, acc, stage, n0, lane, img0 + p0 + wave * R, img0 + pend);
 }
 
 template <int RB, int NT>
-static int launch_conv_mode(const UQKSpatial *d, const ConvArgs &a, dim3 grid)
+static void launch_conv_mode(int mode, const ConvArgs &a, dim3 grid, size_t lds)
 {
-    switch (d->mode) {
+    switch (mode) {
     case UQK_PW: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW>), grid, dim3(256), 0, g_stream, a); break;
     case UQK_G16: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G16>), grid, dim3(256), 0, g_stream, a); break;
     case UQK_G4: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G4>), grid, dim3(256), 0, g_stream, a); break;
-    default: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G1>), grid, dim3(256), 0, g_stream, a); break;
+    case UQK_G1: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G1>), grid, dim3(256), 0, g_stream, a); break;
+    case UQK_ROWS16: hipLaunchKernelGGL((k_conv_rows<RB, NT, false>), grid, dim3(256), lds, g_stream, a); break;
+    default: hipLaunchKernelGGL((k_conv_rows<RB, NT, true>), grid, dim3(256), lds, g_stream, a); break;
     }
-    UQK_LAUNCHED();
-    return 0;
+}
+
+template <int RB>
+static void launch_conv_nt(int nt, int mode, const ConvArgs &a, dim3 grid, size_t lds)
+{
+    switch (nt) {
+    case 2: launch_conv_mode<RB, 2>(mode, a, grid, lds); break;
+    case 4: launch_conv_mode<RB, 4>(mode, a, grid, lds); break;
+    case 6: launch_conv_mode<RB, 6>(mode, a, grid, lds); break;
+    default: launch_conv_mode<RB, 8>(mode, a, grid, lds); break;
+    }
+}
+
+template <int RB>
+static void launch_rows_nt(int nt, int mode, const ConvArgs &a, dim3 grid, size_t lds)
+{
+#define UQK_ROWS_LAUNCH(NT)                                                                                     \
+    do {                                                                                                        \
+        if (mode == UQK_ROWS16) hipLaunchKernelGGL((k_conv_rows<RB, NT, false>), grid, dim3(256), lds, g_stream, a); \
+        else hipLaunchKernelGGL((k_conv_rows<RB, NT, true>), grid, dim3(256), lds, g_stream, a);              \
+    } while (0)
+    switch (nt) {
+    case 2: UQK_ROWS_LAUNCH(2); break;
+    case 4: UQK_ROWS_LAUNCH(4); break;
+    case 6: UQK_ROWS_LAUNCH(6); break;
+    default: UQK_ROWS_LAUNCH(8); break;
+    }
+#undef UQK_ROWS_LAUNCH
+}
+
+// Bytes of dynamic LDS the row-staged kernel needs for one layer.
+extern "C" size_t uqk_conv_rows_lds(const UQKSpatial *d, int rb)
+{
+    const int bm = 4 * 16 * rb;
+    const int span = (bm + d->ow - 2) / d->ow;
+    const int rows_max = span * d->sh + (d->kh - 1) * d->dh + 1;
+    const int cols = (d->ow - 1) * d->sw + (d->kw - 1) * d->dw + 1;
+    const int ndelta = d->mode == UQK_ROWS16 ? d->K / 16 : d->K / 4;
+    const int icp = d->mode == UQK_ROWS16 ? d->ic : (d->ic + 3) & ~3;
+    return (size_t)((rows_max * cols * icp + 15) & ~15) + (size_t)((ndelta * 4 + 15) & ~15) +
+           (size_t)4 * 16 * rb * (16 * d->nt + 16);
 }
 
 extern "C" int uqk_conv(const UQKSpatial *d, const void *x, void *y, uint32_t batches)
@@ -238,29 +499,37 @@ extern "C" int uqk_conv(const UQKSpatial *d, const void *x, void *y, uint32_t ba
     a.w = (const int8_t *)d->w;
     a.epi = (const int4 *)d->epi;
     a.kmap = (const int4 *)d->kmap;
+    a.delta = (const int *)d->kmap;
     a.lut = (const uint8_t *)d->lut;
-    a.M = (int)((uint64_t)batches * d->oh * d->ow);
+    a.M = (long)batches * d->oh * d->ow;
     a.ih = d->ih; a.iw = d->iw; a.ic = d->ic; a.oh = d->oh; a.ow = d->ow; a.oc = d->oc;
-    a.sh = d->sh; a.sw = d->sw; a.pt = d->pt; a.pl = d->pl;
+    a.icp = d->mode == UQK_ROWS4 ? (d->ic + 3) & ~3 : d->ic;
+    a.kh = d->kh; a.sh = d->sh; a.sw = d->sw; a.dh = d->dh; a.pt = d->pt; a.pl = d->pl;
     a.xz = d->xz; a.yz = d->yz; a.lo = d->lo; a.hi = d->hi;
-    a.K = d->K; a.kpad = d->kpad; a.ohw = d->oh * d->ow;
+    a.K = d->K; a.kpad = d->kpad; a.ohw = d->oh * d->ow; a.corr = d->corr;
+    a.cols = (d->ow - 1) * d->sw + (d->kw - 1) * d->dw + 1;
     if (a.M <= 0) return 0;
-    const int rows = 4 * 16 * d->rb;
-    dim3 grid((unsigned)((a.M + rows - 1) / rows), (unsigned)(d->oc_pad / (16 * d->nt)));
-    if (d->rb == 1) {
-        switch (d->nt) {
-        case 2: return launch_conv_mode<1, 2>(d, a, grid);
-        case 4: return launch_conv_mode<1, 4>(d, a, grid);
-        case 6: return launch_conv_mode<1, 6>(d, a, grid);
-        default: return launch_conv_mode<1, 8>(d, a, grid);
-        }
+    const int nchunks = d->oc_pad / (16 * d->nt);
+    if (d->mode == UQK_ROWS16 || d->mode == UQK_ROWS4) {
+        // Larger tiles stage fewer redundant input rows per output row.
+        const int rb = d->mode == UQK_ROWS4 && d->nt <= 4 && uqk_conv_rows_lds(d, 4) <= 65536 ? 4 : 2, bm = 4 * 16 * rb;
+        a.tiles = (a.ohw + bm - 1) / bm;
+        a.rows_max = ((bm + d->ow - 2) / d->ow) * d->sh + (d->kh - 1) * d->dh + 1;
+        dim3 grid((unsigned)((long)batches * a.tiles), (unsigned)nchunks);
+        if (rb == 4) launch_rows_nt<4>(d->nt, d->mode, a, grid, uqk_conv_rows_lds(d, rb));
+        else launch_rows_nt<2>(d->nt, d->mode, a, grid, uqk_conv_rows_lds(d, rb));
+    } else {
+        // Two row blocks per wave only when that still gives every SIMD of
+        // the chip several waves.
+        const long waves2 = (a.M + 31) / 32 * nchunks;
+        const int rb = waves2 >= 8192 ? 2 : 1;
+        const long rows = 4L * 16 * rb;
+        dim3 grid((unsigned)((a.M + rows - 1) / rows), (unsigned)nchunks);
+        if (rb == 2) launch_conv_nt<2>(d->nt, d->mode, a, grid, 0);
+        else launch_conv_nt<1>(d->nt, d->mode, a, grid, 0);
     }
-    switch (d->nt) {
-    case 2: return launch_conv_mode<2, 2>(d, a, grid);
-    case 4: return launch_conv_mode<2, 4>(d, a, grid);
-    case 6: return launch_conv_mode<2, 6>(d, a, grid);
-    default: return launch_conv_mode<2, 8>(d, a, grid);
-    }
+    UQK_LAUNCHED();
+    return 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -274,7 +543,7 @@ struct WinArgs {
     const int4 *epi;
     const uint8_t *lut;
     long total;
-    int groups, ih, iw, c, oh, ow, kh, kw, sh, sw, dh, dw, pt, pl, xz, yz, lo, hi, ohw, is_max;
+    int groups, ih, iw, c, oh, ow, kh, kw, sh, sw, dh, dw, pt, pl, xz, yz, lo, hi, ohw, is_max, corr;
 };
 
 template <int VEC>
@@ -301,7 +570,7 @@ __device__ __forceinline__ void store_vec(int8_t *p, const int *vals)
     else p[0] = (int8_t)words[0];
 }
 
-template <int VEC, bool POOL>
+template <int VEC, bool POOL, int KS>
 __global__ __launch_bounds__(256) void k_window(WinArgs a)
 {
     const long idx = (long)blockIdx.x * 256 + threadIdx.x;
@@ -317,10 +586,13 @@ __global__ __launch_bounds__(256) void k_window(WinArgs a)
 #pragma unroll
     for (int j = 0; j < VEC; j++) acc[j] = POOL && a.is_max ? -128 : 0;
     int count = 0;
-    for (int ky = 0; ky < a.kh; ky++) {
+    const int kh = KS ? KS : a.kh, kw = KS ? KS : a.kw;
+#pragma unroll
+    for (int ky = 0; ky < kh; ky++) {
         const int iy = oy * a.sh - a.pt + ky * a.dh;
         const bool rowin = iy >= 0 && iy < a.ih;
-        for (int kx = 0; kx < a.kw; kx++) {
+#pragma unroll
+        for (int kx = 0; kx < kw; kx++) {
             const int ix = ox * a.sw - a.pl + kx * a.dw;
             const bool in = rowin && ix >= 0 && ix < a.iw;
             int xw[NW];
@@ -339,7 +611,7 @@ __global__ __launch_bounds__(256) void k_window(WinArgs a)
                 }
             } else {
                 int ww[NW];
-                load_vec<VEC>(a.w + (long)(ky * a.kw + kx) * a.c + c0, ww);
+                load_vec<VEC>(a.w + (long)(ky * kw + kx) * a.c + c0, ww);
 #pragma unroll
                 for (int j = 0; j < VEC; j++) {
                     const int xv = VEC >= 4 ? sbyte(xw[j >> 2], j & 3) : (int)(signed char)xw[0];
@@ -361,13 +633,162 @@ __global__ __launch_bounds__(256) void k_window(WinArgs a)
             }
             v = min(max(v, a.lo), a.hi);
         } else {
-            const int4 e = a.epi[c0 + j];
-            v = uq_requant(acc[j], e.x, e.y, e.z, a.yz, a.lo, a.hi);
+            v = uq_requant_affine(acc[j], load_epi(a.epi, c0 + j), a.corr, a.yz, a.lo, a.hi);
             if (a.lut) v = (int)(signed char)a.lut[v + 128];
         }
         out[j] = v;
     }
     store_vec<VEC>(a.y + pix * a.c + c0, out);
+}
+
+// Depthwise with an LDS input tile: a block covers a th x tw patch of output
+// pixels for cg groups of 16 channels of one image. The input patch (halo and
+// padding included, padding written as xz), the block's weights (four taps of
+// one channel per word) and its epilogue records are staged in LDS once. Each
+// thread produces 16 channels of one output pixel: per group of four taps it
+// reads the four 16-byte tap vectors, transposes each 4x4 byte block with
+// v_perm so that a word holds four taps of one channel, and accumulates with
+// v_dot4 (int8 x int8 -> int32), i.e. 12 VALU ops per 16 tap-channel MACs.
+struct DwTileArgs {
+    const int8_t *x;
+    int8_t *y;
+    const int *wdot;
+    const int4 *epi;
+    const uint8_t *lut;
+    int ih, iw, c, oh, ow, sh, sw, dh, dw, pt, pl, xz, yz, lo, hi, corr;
+    int th, tw, cg, tiles_x, ith, itw;
+};
+
+__device__ __forceinline__ void transpose4x4(int x0, int x1, int x2, int x3, int &y0, int &y1, int &y2, int &y3)
+{
+    // perm(s0, s1, sel): byte i of the result is byte sel_i of {s0:s1}, with
+    // indices 0-3 naming s1's bytes and 4-7 naming s0's.
+    const int t0 = (int)__builtin_amdgcn_perm((unsigned)x1, (unsigned)x0, 0x05010400u);
+    const int t1 = (int)__builtin_amdgcn_perm((unsigned)x1, (unsigned)x0, 0x07030602u);
+    const int t2 = (int)__builtin_amdgcn_perm((unsigned)x3, (unsigned)x2, 0x05010400u);
+    const int t3 = (int)__builtin_amdgcn_perm((unsigned)x3, (unsigned)x2, 0x07030602u);
+    y0 = (int)__builtin_amdgcn_perm((unsigned)t2, (unsigned)t0, 0x05040100u);
+    y1 = (int)__builtin_amdgcn_perm((unsigned)t2, (unsigned)t0, 0x07060302u);
+    y2 = (int)__builtin_amdgcn_perm((unsigned)t3, (unsigned)t1, 0x05040100u);
+    y3 = (int)__builtin_amdgcn_perm((unsigned)t3, (unsigned)t1, 0x07060302u);
+}
+
+template <int KS>
+__global__ __launch_bounds__(256) void k_dw_tile(DwTileArgs a)
+{
+    constexpr int TAPS = KS * KS, G = (TAPS + 3) / 4;
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    const int cb = a.cg * 16;
+    const int xbytes = (a.ith * a.itw * cb + 15) & ~15;
+    int8_t *xt = smem;
+    int *wt = (int *)(smem + xbytes);
+    int4 *et = (int4 *)(smem + xbytes + G * cb * 4);
+    const int ty = blockIdx.x / a.tiles_x, tx = blockIdx.x - ty * a.tiles_x;
+    const int c0 = blockIdx.y * cb;
+    const long n = blockIdx.z;
+    const int oy0 = ty * a.th, ox0 = tx * a.tw;
+    const int iy0 = oy0 * a.sh - a.pt, ix0 = ox0 * a.sw - a.pl;
+    const int8_t *xim = a.x + n * a.ih * a.iw * a.c + c0;
+    const int xzw = (a.xz & 0xff) * 0x01010101;
+    const int chunks = a.ith * a.itw * a.cg;
+    for (int q = threadIdx.x; q < chunks; q += 256) {
+        const int p = q / a.cg, g = q - p * a.cg;
+        const int r = p / a.itw, col = p - r * a.itw;
+        const int iy = iy0 + r, ix = ix0 + col;
+        v4i v = {xzw, xzw, xzw, xzw};
+        if (iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw) v = *(const v4i *)(xim + ((long)iy * a.iw + ix) * a.c + g * 16);
+        *(v4i *)(xt + q * 16) = v;
+    }
+    const int wq = cb / 4;
+    for (int q = threadIdx.x; q < G * wq; q += 256) {
+        const int g = q / wq, k = q - g * wq;
+        *(v4i *)(wt + g * cb + 4 * k) = *(const v4i *)(a.wdot + (long)g * a.c + c0 + 4 * k);
+    }
+    for (int q = threadIdx.x; q < 2 * cb; q += 256) et[q] = a.epi[2 * c0 + q];
+    __syncthreads();
+    const int work = a.th * a.tw * a.cg;
+    for (int q = threadIdx.x; q < work; q += 256) {
+        const int p = q / a.cg, gi = q - p * a.cg;
+        const int py = p / a.tw, px = p - py * a.tw;
+        const int oy = oy0 + py, ox = ox0 + px;
+        if (oy >= a.oh || ox >= a.ow) continue;
+        int acc[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) acc[j] = 0;
+        const int8_t *xp = xt + ((py * a.sh) * a.itw + px * a.sw) * cb + gi * 16;
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            v4i X[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int t = 4 * g + j < TAPS ? 4 * g + j : 4 * g;
+                const int ky = t / KS, kx = t - (t / KS) * KS;
+                X[j] = *(const v4i *)(xp + ((ky * a.dh) * a.itw + kx * a.dw) * cb);
+            }
+            const v4i *W = (const v4i *)(wt + g * cb + gi * 16);
+#pragma unroll
+            for (int qd = 0; qd < 4; qd++) {
+                const v4i w4 = W[qd];
+                int y0, y1, y2, y3;
+                transpose4x4(X[0][qd], X[1][qd], X[2][qd], X[3][qd], y0, y1, y2, y3);
+                acc[4 * qd + 0] = __builtin_amdgcn_sdot4(y0, w4[0], acc[4 * qd + 0], false);
+                acc[4 * qd + 1] = __builtin_amdgcn_sdot4(y1, w4[1], acc[4 * qd + 1], false);
+                acc[4 * qd + 2] = __builtin_amdgcn_sdot4(y2, w4[2], acc[4 * qd + 2], false);
+                acc[4 * qd + 3] = __builtin_amdgcn_sdot4(y3, w4[3], acc[4 * qd + 3], false);
+            }
+        }
+        int out[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            int v = uq_requant_affine(acc[j], load_epi(et, gi * 16 + j), a.corr, a.yz, a.lo, a.hi);
+            if (a.lut) v = (int)(signed char)a.lut[v + 128];
+            out[j] = v;
+        }
+        store_vec<16>(a.y + ((n * a.oh + oy) * a.ow + ox) * a.c + c0 + gi * 16, out);
+    }
+}
+
+// Tile geometry for k_dw_tile; returns the dynamic LDS bytes, 0 if unsuited.
+static size_t dw_tile_plan(const UQKSpatial *d, uint32_t batches, DwTileArgs *t)
+{
+    if (d->vec != 16 || d->kh != d->kw || (d->kh != 3 && d->kh != 5) || batches > 65535) return 0;
+    const int groups = d->oc / 16;
+    int cg = 1;
+    for (int c = 4; c >= 1; c--)
+        if (groups % c == 0) { cg = c; break; }
+    const int npx = 256 / cg;
+    const int tw = d->ow < 32 ? d->ow : 32;
+    int th = npx / tw;
+    if (th < 1) th = 1;
+    if (th > d->oh) th = d->oh;
+    t->th = th; t->tw = tw; t->cg = cg;
+    t->tiles_x = (d->ow + tw - 1) / tw;
+    t->ith = (th - 1) * d->sh + (d->kh - 1) * d->dh + 1;
+    t->itw = (tw - 1) * d->sw + (d->kw - 1) * d->dw + 1;
+    const int G = (d->kh * d->kw + 3) / 4;
+    const size_t bytes = (size_t)((t->ith * t->itw * cg * 16 + 15) & ~15) + (size_t)G * cg * 16 * 4 + (size_t)cg * 16 * 32;
+    return bytes <= 65536 ? bytes : 0;
+}
+
+static int launch_dw_tile(const UQKSpatial *d, const void *x, void *y, uint32_t batches)
+{
+    DwTileArgs a;
+    const size_t lds = dw_tile_plan(d, batches, &a);
+    if (!lds) return -1;
+    a.x = (const int8_t *)x;
+    a.y = (int8_t *)y;
+    a.wdot = (const int *)d->wdot;
+    a.epi = (const int4 *)d->epi;
+    a.lut = (const uint8_t *)d->lut;
+    a.ih = d->ih; a.iw = d->iw; a.c = d->oc; a.oh = d->oh; a.ow = d->ow;
+    a.sh = d->sh; a.sw = d->sw; a.dh = d->dh; a.dw = d->dw; a.pt = d->pt; a.pl = d->pl;
+    a.xz = d->xz; a.yz = d->yz; a.lo = d->lo; a.hi = d->hi; a.corr = d->corr;
+    const int tiles_y = (d->oh + a.th - 1) / a.th;
+    dim3 grid((unsigned)(tiles_y * a.tiles_x), (unsigned)(d->oc / (16 * a.cg)), batches);
+    if (d->kh == 3) hipLaunchKernelGGL(k_dw_tile<3>, grid, dim3(256), lds, g_stream, a);
+    else hipLaunchKernelGGL(k_dw_tile<5>, grid, dim3(256), lds, g_stream, a);
+    UQK_LAUNCHED();
+    return 0;
 }
 
 static int launch_window(const UQKSpatial *d, const void *x, void *y, uint32_t batches, bool pool)
@@ -383,26 +804,35 @@ static int launch_window(const UQKSpatial *d, const void *x, void *y, uint32_t b
     a.pt = d->pt; a.pl = d->pl; a.xz = d->xz; a.yz = d->yz; a.lo = d->lo; a.hi = d->hi;
     a.ohw = d->oh * d->ow;
     a.is_max = d->is_max;
+    a.corr = d->corr;
     const int vec = d->vec;
     a.groups = d->oc / vec;
     a.total = (long)batches * a.ohw * a.groups;
     if (a.total <= 0) return 0;
     dim3 grid((unsigned)((a.total + 255) / 256));
+    const int ks = d->kh == d->kw && (d->kh == 3 || d->kh == 5) ? d->kh : 0;
+#define UQK_WIN(V, P, K) hipLaunchKernelGGL((k_window<V, P, K>), grid, dim3(256), 0, g_stream, a)
+#define UQK_WIN_KS(V, P) do { if (ks == 3) UQK_WIN(V, P, 3); else if (ks == 5) UQK_WIN(V, P, 5); else UQK_WIN(V, P, 0); } while (0)
     if (pool) {
-        if (vec == 16) hipLaunchKernelGGL((k_window<16, true>), grid, dim3(256), 0, g_stream, a);
-        else if (vec == 4) hipLaunchKernelGGL((k_window<4, true>), grid, dim3(256), 0, g_stream, a);
-        else hipLaunchKernelGGL((k_window<1, true>), grid, dim3(256), 0, g_stream, a);
+        if (vec == 16) UQK_WIN_KS(16, true);
+        else if (vec == 4) UQK_WIN_KS(4, true);
+        else UQK_WIN_KS(1, true);
     } else {
-        if (vec == 16) hipLaunchKernelGGL((k_window<16, false>), grid, dim3(256), 0, g_stream, a);
-        else if (vec == 4) hipLaunchKernelGGL((k_window<4, false>), grid, dim3(256), 0, g_stream, a);
-        else hipLaunchKernelGGL((k_window<1, false>), grid, dim3(256), 0, g_stream, a);
+        if (vec == 16) UQK_WIN_KS(16, false);
+        else if (vec == 4) UQK_WIN_KS(4, false);
+        else UQK_WIN_KS(1, false);
     }
+#undef UQK_WIN_KS
+#undef UQK_WIN
     UQK_LAUNCHED();
     return 0;
 }
 
 extern "C" int uqk_depthwise(const UQKSpatial *d, const void *x, void *y, uint32_t batches)
 {
+    if (!batches) return 0;
+    const int rc = launch_dw_tile(d, x, y, batches);
+    if (rc >= 0) return rc;
     return launch_window(d, x, y, batches, false);
 }
 

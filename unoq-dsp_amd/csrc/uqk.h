@@ -15,22 +15,32 @@ extern "C" {
  * load time by graph.c:
  *   w    conv: [oc_pad][kpad] signed int8, k = (ky, kx, ic), zero beyond K
  *        depthwise: [taps][C] signed int8 (the plan's own layout)
- *   epi  int32 x4 per channel: corrected bias folded for signed inputs
- *        (bias + 128*sum(w) [+ xz*tail weights]), multiplier, shift, 0
+ *   epi  32 bytes per channel: corrected bias folded for signed inputs
+ *        (bias + 128*sum(w) [+ xz*tail weights]), multiplier, left shift,
+ *        total right shift, and two int64 constants of the one-multiply
+ *        requantisation (see epilogue_record in graph.c)
+ *   wdot depthwise: [ceil(taps/4)][C] words of four taps per channel
  *   kmap conv gathers: int32 x4 per gather group {ky*dh, kx*dw, ic, 0}
  *   lut  optional fused 256-entry post table (uq_post) */
 typedef struct {
     int32_t ih, iw, ic, oh, ow, oc;
     int32_t kh, kw, sh, sw, dh, dw, pt, pl;
     int32_t xz, yz, lo, hi;
-    int32_t K, kpad, oc_pad, mode, nt, rb, is_max, vec;
+    int32_t K, kpad, oc_pad, mode, nt, rb, is_max, vec, corr;
     const void *w;
+    const void *wdot;
     const void *epi;
     const void *kmap;
     const void *lut;
 } UQKSpatial;
 
-enum { UQK_PW = 0, UQK_G16 = 1, UQK_G4 = 2, UQK_G1 = 3 };
+/* Conv A-operand sources: pointwise rows, per-lane gathers with 16/4/1-byte
+ * granularity, or LDS-staged input rows (16-byte slices, or 4-byte words
+ * over channels padded to a multiple of four). */
+enum { UQK_PW = 0, UQK_G16 = 1, UQK_G4 = 2, UQK_G1 = 3, UQK_ROWS16 = 4, UQK_ROWS4 = 5 };
+
+/* Dynamic LDS bytes k_conv_rows needs for a layer at rb row blocks per wave. */
+size_t uqk_conv_rows_lds(const UQKSpatial *d, int rb);
 
 int uqk_init(void);
 int uqk_device_count(void);
