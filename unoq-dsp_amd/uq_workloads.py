@@ -110,6 +110,17 @@ def conv3x3(seed=5, images=512):
     return p.build(z), images
 
 
+def lutcopy(seed=6, images=16):
+    """Identity 256-entry lookup over 4 MiB per image: a plain streaming copy
+    kernel of known size (reads and writes images * 4 MiB), used to calibrate
+    the HBM byte counters."""
+    p = Plan(seed)
+    x = p.input((1, 1024, 1024, 4), zp=0)
+    table = p.lut_table(np.arange(256, dtype=np.int64) ^ 128)
+    z = p.lut(x, table)
+    return p.build(z), images
+
+
 WORKLOADS = {
     "pointwise": pointwise,
     "dw3s1": lambda **kw: depthwise("dw3s1", **kw),
@@ -119,4 +130,5 @@ WORKLOADS = {
     "mnv4": mnv4,
     "head": head,
     "conv3x3": conv3x3,
+    "lutcopy": lutcopy,
 }
