@@ -119,6 +119,18 @@ def roofline_entry(costs, per_op_ns):
                "algorithmic_bytes": c["bytes"], "algorithmic_ops": c["ops"], "avg_ns": round(float(per_op_ns[i]), 1)}
 
 
+def committed_traffic(workload, op):
+    """HBM bytes per launch of `op`, from the rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary committed under profiles/ (None when no summary covers it)."""
+    for path in sorted((ROOT / "profiles").glob("*traffic*.txt")):
+        for line in path.read_text().splitlines():
+            if line.startswith("machine:"):
+                kv = dict(item.split("=", 1) for item in line.split()[1:])
+                if kv.get("workload") == workload and int(kv.get("op", -1)) == op:
+                    return int(kv["traffic_bytes"]), path.name
+    return None, None
+
+
 def secondary(lib, steps):
     out = {}
     for name in ("head", "conv3x3"):
@@ -166,7 +178,11 @@ def main():
             log(f"op {i:3d} code {c['code']:2d} {ns / 1e3:9.2f} us  {c['bytes'] / ns:8.1f} GB/s  "
                 f"{(c['ops'] / ns / 1e3 if c['ops'] else 0):8.1f} TOP/s")
         log(f"sum of op times {per_op_ns.sum() / 1e3:.1f} us, wall per step {seconds / args.steps * 1e6:.1f} us")
-    _, roof = roofline_entry(costs, per_op_ns)
+    op, roof = roofline_entry(costs, per_op_ns)
+    traffic, source = committed_traffic(args.workload, op)
+    if traffic:
+        roof["traffic"] = traffic
+        roof["traffic_source"] = f"profiles/{source}"
     ms = seconds / args.steps * 1e3
     result = {
         "metric": METRIC, "value": round(images * args.steps / seconds, 1), "unit": "images/s",
