@@ -10,8 +10,9 @@ Prints ONE JSON line. Besides the headline images/s it reports:
                 bytes (or ops) per launch over its HIP-event duration
   cpu_baseline  the reference's portable C runtime (oracle/_ref, built from
                 the reference sources) on this host's cores, batch-1 plans
-  secondary     int8 conv TOPS (1x1 head GEMM, 3x3 implicit GEMM, batch 512)
-                and depthwise HBM GB/s (four cases, batch 64)
+  secondary     YOLO26n-shaped detector images/s (320x320, batch 64), int8
+                conv TOPS (1x1 head GEMM, 3x3 implicit GEMM, batch 512) and
+                depthwise HBM GB/s (four cases, batch 64)
 """
 import argparse
 import ctypes as C
@@ -133,6 +134,11 @@ def committed_traffic(workload, op):
 
 def secondary(lib, steps):
     out = {}
+    plan, images = W.WORKLOADS["yolo"]()
+    g = Graph(plan, lib)
+    sec, per_op = time_device(lib, g, images, steps, 2)
+    out["yolo"] = {"images": images, "ms": round(sec / steps * 1e3, 4), "images_per_s": round(images * steps / sec, 1),
+                   "gops": round(sum(c["ops"] for c in P.op_costs(plan, images)) / 1e9, 2)}
     for name in ("head", "conv3x3"):
         plan, images = W.WORKLOADS[name]()
         g = Graph(plan, lib)

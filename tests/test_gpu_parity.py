@@ -34,7 +34,8 @@ def _assert_same(got, want, what):
 
 
 @pytest.mark.parametrize("name,images", [("pointwise", 1), ("pointwise", 3), ("dw3s1", 64), ("dw3s2", 64),
-                                         ("dw5s1", 64), ("dw5s2", 64), ("head", 16), ("conv3x3", 2), ("mnv4", 3)])
+                                         ("dw5s1", 64), ("dw5s2", 64), ("head", 16), ("conv3x3", 2), ("mnv4", 3),
+                                         ("yolo", 2)])
 def test_workload_bit_exact(lib, name, images):
     plan, _ = W.WORKLOADS[name]()
     x = P.random_input(plan, images, 21)
@@ -48,7 +49,7 @@ def test_single_image_entry_point(lib):
     _assert_same(Graph(plan, lib).run(x), _oracle(plan, x, 1), "ug_run")
 
 
-@pytest.mark.parametrize("name,images,samples", [("mnv4", 256, (0, 137, 255)), ("head", 512, (0, 511)),
+@pytest.mark.parametrize("name,images,samples", [("mnv4", 256, (0, 137, 255)), ("yolo", 64, (0, 63)), ("head", 512, (0, 511)),
                                                  ("conv3x3", 512, (5, 400))])
 def test_full_batch_sampled_images(lib, name, images, samples):
     plan, _ = W.WORKLOADS[name]()

@@ -34,7 +34,8 @@ def _check_plan(plan, images, seed):
 
 
 @pytest.mark.parametrize("name,images", [("pointwise", 2), ("dw3s1", 2), ("dw3s2", 2), ("dw5s1", 2),
-                                         ("dw5s2", 2), ("head", 3), ("conv3x3", 1), ("mnv4", 1)])
+                                         ("dw5s2", 2), ("head", 3), ("conv3x3", 1), ("mnv4", 1),
+                                         ("yolo", 1)])
 def test_workloads_match_reference(name, images):
     plan, _ = W.WORKLOADS[name]()
     y = _check_plan(plan, images, seed=11)
