@@ -91,6 +91,23 @@ int ug_device_download(void *dst, const void *d_src, uint64_t bytes);
 /* Number of ops of the loaded plan, 0 when not loaded. */
 uint32_t ug_op_count(void);
 
+/* ---- Part 3: .uqmodel bundles (src/unoq_dsp/bundle.py:18-19, 84-141) ---- */
+
+/* Check a bundle image (header, lengths, SHA-256 of manifest || plan, plan
+ * magic and version 2/3) and return a pointer into it at the plan. Returns 0,
+ * 30 for a bad header or length, 31 for a checksum mismatch, 32 for a plan the
+ * bundle format does not admit. The Python loader raises InvalidBundle in
+ * these cases; the C ABI reports them as codes above the loader's range. */
+int ug_bundle_plan(const void *file, uint64_t len, const void **plan, uint32_t *plan_len);
+
+/* ug_bundle_plan, then ug_load on the plan (returning ug_load's code). A
+ * bundle error leaves any previously loaded model in place, as the Python
+ * loader fails before reaching the runtime. */
+int ug_load_bundle(const void *file, uint64_t len);
+
+/* SHA-256 of a byte string (FIPS 180-4), the bundle checksum. */
+void uq_sha256(const void *data, uint64_t len, uint8_t out[32]);
+
 #ifdef __cplusplus
 }
 #endif

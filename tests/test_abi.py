@@ -16,7 +16,7 @@ ROOT = Path(__file__).resolve().parents[1]
 def declared_functions():
     text = (ROOT / "include" / "uq_graph.h").read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return set(re.findall(r"\b(ug_\w+)\s*\(", text))
+    return set(re.findall(r"\b((?:ug|uq)_\w+)\s*\(", text))
 
 
 def test_header_and_binding_agree():
@@ -25,7 +25,7 @@ def test_header_and_binding_agree():
 
 def test_library_exports_every_declared_symbol():
     out = subprocess.run(["nm", "-D", "--defined-only", str(DEFAULT_LIBRARY)], capture_output=True, text=True, check=True).stdout
-    exported = set(re.findall(r" T (ug_\w+)", out))
+    exported = set(re.findall(r" T ((?:ug|uq)_\w+)", out))
     missing = declared_functions() - exported
     assert not missing, missing
 

@@ -34,6 +34,9 @@ SIGNATURES = [
     ("ug_device_upload", C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64]),
     ("ug_device_download", C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64]),
     ("ug_op_count", C.c_uint32, []),
+    ("ug_bundle_plan", C.c_int, [C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p), C.POINTER(C.c_uint32)]),
+    ("ug_load_bundle", C.c_int, [C.c_void_p, C.c_uint64]),
+    ("uq_sha256", None, [C.c_void_p, C.c_uint64, C.c_void_p]),
 ]
 
 
