@@ -142,6 +142,99 @@ static void mean_image(const int8_t *x, int8_t *y, unsigned batches, unsigned ch
         }
 }
 
+/* uq_mul, qnn.c:111-116: elementwise product of zero-point-shifted operands,
+ * one requant, clamp to [q5, q6]. */
+static void mul_image(const int8_t *x, const int8_t *b, int8_t *y, uint32_t count, const int32_t *q)
+{
+    for (uint32_t i = 0; i < count; i++) {
+        int32_t prod = ((int32_t)x[i] - q[0]) * ((int32_t)b[i] - q[1]);
+        y[i] = clampi((int64_t)uqo_scale(prod, q[3], q[4]) + q[2], q[5], q[6]);
+    }
+}
+
+/* uq_bmm, qnn.c:117-153: for each of the d0 matrices, z[r][c] =
+ * clamp(scale(sum_t (A[r][t] - q0) * (B[t][c] - q1), q3, q4) + q2). q5 = 1
+ * reads A as [k][m], q6 = 1 reads B as [n][k]. The reference forms the same
+ * exact integer sum from a u8 x i8 product and three correction terms
+ * (qnn.c:142); the loader bounds it to int32 (graph.c:189). */
+static void bmm_image(const Ten *a, const Ten *b, const Ten *z, const int8_t *x, const int8_t *w, int8_t *y, const int32_t *q)
+{
+    unsigned batches = z->d[0], m = z->d[1], n = z->d[2], k = a->d[q[5] ? 1 : 2];
+    for (unsigned h = 0; h < batches; h++) {
+        const int8_t *xa = x + (size_t)h * m * k, *wb = w + (size_t)h * k * n;
+        for (unsigned r = 0; r < m; r++)
+            for (unsigned c = 0; c < n; c++) {
+                int64_t acc = 0;
+                for (unsigned t = 0; t < k; t++) {
+                    int av = xa[q[5] ? (size_t)t * m + r : (size_t)r * k + t];
+                    int bv = wb[q[6] ? (size_t)c * k + t : (size_t)t * n + c];
+                    acc += (int64_t)(av - q[0]) * (bv - q[1]);
+                }
+                y[((size_t)h * m + r) * n + c] = clampi((int64_t)uqo_scale((int32_t)acc, q[3], q[4]) + q[2], -128, 127);
+            }
+    }
+    (void)b;
+}
+
+/* Rounding doubling high multiply, qnn.c:61-70 with shift 0. */
+static int32_t high_mul(int32_t a, int32_t b) { return uqo_scale(a, b, 0); }
+
+/* uq_softmax_exact, qnn.c:87-107. Per row of q[0] values: e_j = lut[max - x_j]
+ * (Q0.31 exponentials), S = sum of e_j rounded to Q12, 1/S by a fixed-point
+ * Newton-Raphson iteration on S normalised to [1, 2) (gemmlowp's
+ * one_over_one_plus_x_for_x_in_0_1: start 48/17 - 32/17 x, three steps
+ * r += r (1 - x r)), then y_j = round(r e_j / 2^exponent) - 128, 127 on
+ * overflow. */
+static void softmax_image(const int8_t *x, int8_t *y, uint32_t bytes, const int32_t *q)
+{
+    uint32_t width = (uint32_t)q[0];
+    const int32_t *lut = q + 1;
+    for (uint32_t base = 0; base < bytes; base += width) {
+        int mx = -128;
+        for (uint32_t j = 0; j < width; j++) if (x[base + j] > mx) mx = x[base + j];
+        uint32_t sum = 0;
+        for (uint32_t j = 0; j < width; j++) sum += ((uint32_t)lut[mx - x[base + j]] + 2048u) >> 12;
+        unsigned lead = 0;
+        while (!(sum & (0x80000000u >> lead))) lead++;
+        unsigned exponent = 35 - lead;
+        uint32_t frac = (sum << lead) - 0x80000000u;              /* (S / 2^(31-lead) - 1) in Q0.32 */
+        int32_t half = (int32_t)(((uint64_t)frac + 0x80000000u) >> 1); /* (1 + frac) / 2 in Q0.31 */
+        int32_t r = 1515870810 + high_mul(half, -1010580540);     /* 48/17 - 32/17 * half, Q2.29 */
+        for (int it = 0; it < 3; it++) {
+            int32_t err = 536870912 - high_mul(half, r);         /* 1 - half * r, Q2.29 */
+            r += high_mul(r, err) * 4;
+        }
+        int64_t r2 = (int64_t)r * 2;
+        r = r2 > 2147483647 ? 2147483647 : (int32_t)r2;
+        for (uint32_t j = 0; j < width; j++) {
+            uint32_t v = (uint32_t)high_mul(r, lut[mx - x[base + j]]);
+            uint32_t rounded = exponent >= 32 ? 0 : (v + (1u << (exponent - 1))) >> exponent;
+            y[base + j] = (int8_t)(rounded > 255 ? 127 : (int)rounded - 128);
+        }
+    }
+}
+
+/* Code 10, graph.c:374-390: z[i0..] = a[...] with z->d[d] = a->d[p[d]], for
+ * any element width (the two float NHWC/NCHW cases there are instances of
+ * the same permutation). */
+static void transpose_image(const Ten *a, const Ten *z, const uint8_t *x, uint8_t *y, const uint32_t *perm)
+{
+    unsigned w = a->type == 1 || a->type == 4 ? 4 : 1, rank = a->rank;
+    size_t astride[4], count = 1;
+    size_t acc = 1;
+    for (int d = (int)rank - 1; d >= 0; d--) { astride[d] = acc; acc *= a->d[d]; }
+    for (unsigned d = 0; d < rank; d++) count *= z->d[d];
+    for (size_t e = 0; e < count; e++) {
+        size_t rem = e, src = 0;
+        for (int d = (int)rank - 1; d >= 0; d--) {
+            size_t idx = rem % z->d[d];
+            rem /= z->d[d];
+            src += idx * astride[perm[d]];
+        }
+        memcpy(y + e * w, x + src * w, w);
+    }
+}
+
 int uqo_run(const void *plan, uint32_t len, const void *input, uint32_t images,
             void *output, uint32_t snap_tensor, void *snap_out)
 {
@@ -185,6 +278,10 @@ int uqo_run(const void *plan, uint32_t len, const void *input, uint32_t images,
             case 18: add_image(ap, bp, zp, z->bytes, (const int32_t *)CONST(o->p[0])); break;
             case 24: mean_image(ap, zp, a->d[0], a->d[3], (const int32_t *)bp); break;
             case 5: memcpy(zp, ap, z->bytes); break;                                   /* graph.c:408 */
+            case 10: transpose_image(a, z, (const uint8_t *)ap, (uint8_t *)zp, o->p); break;
+            case 25: mul_image(ap, bp, zp, z->bytes, (const int32_t *)CONST(o->p[0])); break;
+            case 27: bmm_image(a, b, z, ap, bp, zp, (const int32_t *)CONST(o->p[0])); break;
+            case 28: softmax_image(ap, zp, z->bytes, (const int32_t *)bp); break;
             case 22: {                                                                 /* graph.c:331-341 */
                 const uint8_t *table = (const uint8_t *)bp;
                 unsigned flip = a->type == 3 ? 128 : 0;

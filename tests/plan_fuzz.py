@@ -2,7 +2,9 @@
 edge-case geometry: odd channel counts, 1xN kernels, strides 1-3, dilation,
 explicit and SAME padding, K tails with nonzero weights, positive shifts,
 zero multipliers, fused post tables, batch/channel padding, slices, concat on
-every axis, resize, pooling, mean and packed outputs."""
+every axis, resize, pooling, mean, packed outputs, elementwise products,
+permutations and attention (batched matmul with either operand transposed,
+exact softmax)."""
 import numpy as np
 
 from uq_plan import Plan, Rng
@@ -119,18 +121,87 @@ def concat_op(p, rng, x):
     return p.concat(x, other, axis=_pick(rng, [0, 1, 2, 3, 3]))
 
 
-OPS = [conv_op, conv_op, conv_op, dw_op, dw_op, pool_op, pad_op, slice_op, resize_op, add_op, concat_op]
+def mul_op(p, rng, x):
+    other = p.lut(x, _random_lut(p, rng)) if _pick(rng, [0, 1]) else x
+    return p.mul(x, other, act=_pick(rng, ["none", "relu"]))
 
 
-def random_plan(seed, max_ops=4):
-    """A small random chain; returns (plan bytes, per-image input bytes)."""
+def transpose_op(p, rng, x):
+    """A 4-D permutation and its inverse, so the chain stays NHWC-shaped."""
+    perm = [int(v) for v in np.argsort(rng.uniform01(4))]
+    y = p.transpose(x, perm)
+    if _pick(rng, [0, 1]):
+        y = p.lut(y, _random_lut(p, rng))
+    inverse = [perm.index(d) for d in range(4)]
+    return p.transpose(y, inverse)
+
+
+def attention_op(p, rng, x):
+    """Self-attention on rank-3 views, as the detector's attention block:
+    S = bmm(Q, K^T), P = softmax(S), O = bmm(V, P^T) or bmm(P, V)."""
+    n, h, w, c = p.shape(x)
+    q = p.copy(x, (n * h, w, c))
+    kq = p.lut(q, _random_lut(p, rng))
+    kt_stored = _pick(rng, [0, 1])
+    k_op = kq if kt_stored else p.transpose(kq, (0, 2, 1))            # [B][N][K] or [B][K][N]
+    ta = _pick(rng, [0, 0, 1])
+    a = p.transpose(q, (0, 2, 1)) if ta else q
+    scores = p.bmm(a, k_op, trans_a=bool(ta), trans_b=bool(kt_stored))   # [B][w][w]
+    probs = p.softmax(scores)
+    v = p.lut(q, _random_lut(p, rng))                                  # [B][w][c]
+    out = p.bmm(probs, v)                                              # [B][w][c]
+    return p.copy(out, (n, h, w, c))
+
+
+def _constant_like(p, rng, shape):
+    t = p.tensor(shape, values=rng.int8(int(np.prod(shape))))
+    p.zp[t] = int(rng.integers(1, -128, 127)[0])
+    return t
+
+
+def constant_operand_op(p, rng, x):
+    """A constant tensor in a slot the runtime reads image by image: the
+    second operand of add / concat / mul, or the input of a LUT or copy
+    (graph.c:72 admits any defined tensor there, constants included)."""
+    kind = _pick(rng, ["add", "concat", "mul", "lut", "copy"])
+    c = _constant_like(p, rng, p.shape(x))
+    if kind == "add":
+        return p.add(x, c) if _pick(rng, [0, 1]) else p.add(c, x)
+    if kind == "concat":
+        return p.concat(x, c, axis=_pick(rng, [0, 1, 2, 3]))
+    if kind == "mul":
+        return p.mul(x, c)
+    y = p.lut(c, _random_lut(p, rng)) if kind == "lut" else p.copy(c)
+    return p.add(x, y)
+
+
+def constant_bmm_op(p, rng, x):
+    """bmm with a constant right-hand matrix, as a compiled BATCH_MATMUL with
+    a weight buffer (tests/test_modern_ops.py:87-94 pattern)."""
+    n, h, w, c = p.shape(x)
+    a = p.copy(x, (n * h, w, c))
+    tb = _pick(rng, [0, 1])
+    cols = _pick(rng, [1, 3, 8, 17, 32, 33])
+    b = _constant_like(p, rng, (n * h, cols, c) if tb else (n * h, c, cols))
+    z = p.bmm(a, b, trans_b=bool(tb))
+    return p.copy(z, (n, h, w, cols))
+
+
+OPS = [conv_op, conv_op, conv_op, dw_op, dw_op, pool_op, pad_op, slice_op, resize_op, add_op, concat_op,
+       mul_op, transpose_op, attention_op]
+ATTENTION_OPS = [attention_op, attention_op, transpose_op, mul_op, conv_op, constant_bmm_op]
+CONSTANT_OPS = [constant_operand_op, constant_operand_op, constant_bmm_op, conv_op, dw_op]
+
+
+def random_plan(seed, max_ops=4, ops=None):
+    """A small random chain (plan bytes) drawn from `ops` (default: all)."""
     rng = Rng(seed, 424242)
     p = Plan(seed)
     shape = (int(_pick(rng, [1, 1, 2])), int(rng.integers(1, 1, 12)[0]), int(rng.integers(1, 1, 12)[0]),
              int(_pick(rng, [1, 2, 3, 4, 8, 12, 16, 24, 32, 48, 64])))
     t = p.input(shape, zp=int(rng.integers(1, -128, 127)[0]))
     for _ in range(int(rng.integers(1, 1, max_ops)[0])):
-        t = _pick(rng, OPS)(p, rng, t)
+        t = _pick(rng, OPS if ops is None else ops)(p, rng, t)
     tail = _pick(rng, ["none", "mean", "pack", "copy"])
     if tail == "mean":
         t = p.mean(t, keepdims=bool(_pick(rng, [0, 1])), scale_ratio=float(0.3 + rng.uniform01(1)[0]))

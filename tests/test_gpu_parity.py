@@ -10,7 +10,8 @@ import pytest
 
 import uq_plan as P
 import uq_workloads as W
-from plan_fuzz import random_plan
+from plan_fuzz import ATTENTION_OPS, CONSTANT_OPS, random_plan
+from test_oracle_vs_reference import BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, transpose_plan
 from refs import oracle_run
 from uq_native import DeviceBuffer, Graph, NativeError, open_library
 
@@ -76,6 +77,49 @@ def test_random_plans(lib, seed):
     images = 3
     x = P.random_input(plan, images, seed)
     _assert_same(Graph(plan, lib).run_batch(x, images), _oracle(plan, x, images), f"random plan {1000 + seed}")
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_attention_plans(lib, seed):
+    plan = random_plan(7000 + seed, ops=ATTENTION_OPS)
+    images = 3
+    x = P.random_input(plan, images, seed)
+    _assert_same(Graph(plan, lib).run_batch(x, images), _oracle(plan, x, images), f"attention plan {7000 + seed}")
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_constant_operand_plans(lib, seed):
+    """Constants in per-image operand slots, several images per batch."""
+    plan = random_plan(8000 + seed, ops=CONSTANT_OPS)
+    images = 5
+    x = P.random_input(plan, images, seed)
+    _assert_same(Graph(plan, lib).run_batch(x, images), _oracle(plan, x, images), f"constant-operand plan {8000 + seed}")
+
+
+@pytest.mark.parametrize("width", [1, 3, 17, 100, 256, 512, 2048])
+@pytest.mark.parametrize("beta_scale", [0.001, 0.17, 16.0])
+def test_softmax(lib, width, beta_scale):
+    plan = softmax_plan(width, beta_scale)
+    images = 7
+    x = P.random_input(plan, images, width)
+    x[:3 * width] = np.repeat(np.array([-128, 0, 127], np.int8), width)   # all-tie rows
+    _assert_same(Graph(plan, lib).run_batch(x, images), _oracle(plan, x, images), f"softmax w={width}")
+
+
+@pytest.mark.parametrize("shape,perm", TRANSPOSES)
+def test_transpose(lib, shape, perm):
+    plan = transpose_plan(shape, perm)
+    x = P.random_input(plan, 4, 2)
+    _assert_same(Graph(plan, lib).run_batch(x, 4), _oracle(plan, x, 4), f"transpose {shape} {perm}")
+
+
+@pytest.mark.parametrize("shape", BMM_SHAPES + [(3, 100, 32, 100), (1, 5, 8192, 3), (2, 3, 40, 2048)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_bmm(lib, shape, ta, tb):
+    plan = bmm_plan(*shape, bool(ta), bool(tb))
+    images = 3
+    x = P.random_input(plan, images, 6)
+    _assert_same(Graph(plan, lib).run_batch(x, images), _oracle(plan, x, images), f"bmm {shape} {ta}{tb}")
 
 
 def test_snapshot_intermediate(lib):

@@ -4,19 +4,30 @@ runtime compiled from its sources (oracle/_ref), in both the release macro set
 constant-channel elimination, fixed depthwise kernels) and the plain build.
 
 Pins: conv_image (code 14), window_image (codes 15 and 16), add_image,
-mean_image, and the byte ops 5/19/20/21/22/23/26 of uqo_run. The reference's
+mean_image, mul_image (25), bmm_image (27), softmax_image (28),
+transpose_image (10) and the byte ops 5/19/20/21/22/23/26 of uqo_run, plus
+the whole of both shipped models (MobileNetV4-small, YOLO26n-320 with its
+attention block) where the reference tree is present. The reference's
 known-answer patterns are re-scored here by the reference C build, since
 their LiteRT expected values cannot run offline:
   * test_residual_add.py:64-96  every int8 pair x 4 scale cases x 3 clamps
   * test_modern_ops.py:166-173  requantisation ties with identity weights
+  * test_modern_ops.py:59-64    softmax widths 1..256 x five input scales
+  * test_modern_ops.py:75-79    transposes of ranks 2, 3 and 4
+  * test_modern_ops.py:87-94    bmm shapes x all four transpose flags
 """
+import struct
+from pathlib import Path
+
 import numpy as np
 import pytest
 
 import uq_plan as P
 import uq_workloads as W
-from plan_fuzz import random_plan
+from plan_fuzz import ATTENTION_OPS, CONSTANT_OPS, random_plan
 from refs import oracle_run, ref_plain, ref_release
+
+MODELS = Path("/root/reference/models")
 
 
 def _check_plan(plan, images, seed):
@@ -97,3 +108,81 @@ def test_requant_ties_identity_conv(exponent, fraction, zero):
     rel = ref_release()
     assert rel.load(plan) == 0
     np.testing.assert_array_equal(oracle_run(plan, xin, 1, 2048), rel.run_images(xin, 1))
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_attention_plans_match_reference(seed):
+    _check_plan(random_plan(7000 + seed, ops=ATTENTION_OPS), 2, seed)
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_constant_operand_plans_match_reference(seed):
+    _check_plan(random_plan(8000 + seed, ops=CONSTANT_OPS), 3, seed)
+
+
+def softmax_plan(width, beta_scale, rows=3, zp=-17):
+    p = P.Plan(width)
+    x = p.input((rows, width), zp=zp)
+    return p.build(p.softmax(x, beta_scale=beta_scale))
+
+
+@pytest.mark.parametrize("width", [1, 2, 3, 17, 100, 256, 511, 512, 2048])
+@pytest.mark.parametrize("beta_scale", [0.001, 0.03, 0.17, 1.0, 16.0])
+def test_softmax_widths_and_scales(width, beta_scale):
+    plan = softmax_plan(width, beta_scale)
+    _check_plan(plan, 2, width)
+    # Rows of one repeated value (ties everywhere; the widest rows reach the
+    # exponent >= 32 branch).
+    xin = np.repeat(np.array([-128, 0, 127], np.int8), width)
+    rel = ref_release()
+    assert rel.load(plan) == 0
+    np.testing.assert_array_equal(oracle_run(plan, xin, 1, P.output_bytes(plan)), rel.run_images(xin, 1))
+
+
+TRANSPOSES = [((2, 3), (1, 0)), ((2, 3, 5), (0, 2, 1)), ((2, 3, 5, 7), (0, 3, 1, 2)), ((2, 3, 5, 7), (0, 2, 3, 1)),
+              ((1, 2, 32, 100), (0, 1, 3, 2)), ((3, 1, 4, 2), (3, 2, 0, 1))]
+
+
+def transpose_plan(shape, perm):
+    p = P.Plan(len(shape))
+    x = p.input(shape, zp=-19)
+    return p.build(p.transpose(x, perm))
+
+
+@pytest.mark.parametrize("shape,perm", TRANSPOSES)
+def test_transpose_ranks(shape, perm):
+    _check_plan(transpose_plan(shape, perm), 2, 3)
+
+
+BMM_SHAPES = [(2, 7, 11, 9), (2, 33, 32, 35), (2, 64, 100, 100)]
+
+
+def bmm_plan(batches, m, k, n, ta, tb, seed=98):
+    p = P.Plan(seed)
+    x = p.input((batches, k, m) if ta else (batches, m, k), zp=2)
+    rng = P.Rng(seed, 5)
+    bsh = (batches, n, k) if tb else (batches, k, n)
+    b = p.tensor(bsh, values=rng.int8(int(np.prod(bsh))))
+    p.zp[b] = -17
+    return p.build(p.bmm(x, b, trans_a=ta, trans_b=tb, yz=-19))
+
+
+@pytest.mark.parametrize("shape", BMM_SHAPES)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_bmm_shapes_and_transposes(shape, ta, tb):
+    _check_plan(bmm_plan(*shape, bool(ta), bool(tb)), 2, 4)
+
+
+def real_plan(name):
+    path = MODELS / name
+    if not path.exists():
+        pytest.skip("reference models not present")
+    data = path.read_bytes()
+    nm = struct.unpack_from("<I", data, 12)[0]
+    return data[52 + nm:]
+
+
+@pytest.mark.parametrize("name", ["mobilenetv4-small.uqmodel", "yolo26n-320.uqmodel"])
+def test_shipped_models_match_reference(name):
+    y = _check_plan(real_plan(name), 2, 17)
+    assert len(np.unique(y)) > 16

@@ -3,8 +3,9 @@
 headers, tensor records, op records, parameter blocks and weights, plus
 version-3 lifetime overlaps. Validation runs on the host before any GPU work,
 so this test needs no GPU: a plan the reference accepts gets 0 on a GPU host,
-24 where no GPU is present, and 19 when it uses ops outside the INT8 vision
-path that the reference runtime also implements (float ops, transposes...).
+24 where no GPU is present, and 19 when it uses ops outside the INT8 path
+that the reference runtime also implements (float ops and float / u8 x i8
+matmuls, codes 1-4 and 6-9, 11-13).
 
 The reference side is the plain build (no macros); the release build's load
 path adds its own preparation steps and is compared on the unmutated plans.
@@ -20,7 +21,7 @@ from plan_fuzz import random_plan
 from refs import ref_plain, ref_release
 from uq_native import open_library
 
-SUPPORTED = {5, 14, 15, 16, 18, 19, 20, 21, 22, 23, 24, 26}
+SUPPORTED = {5, 10, 14, 15, 16, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28}
 
 
 @pytest.fixture(scope="module")

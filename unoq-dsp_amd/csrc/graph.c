@@ -40,6 +40,7 @@ static struct {
     uint8_t *dev_prep;           /* device pool of prepared per-op tables */
     uint8_t *act[UG_MAX_T];      /* device activation buffers, capacity images each */
     uint8_t *ptr[UG_MAX_T];      /* per-run tensor addresses */
+    uint8_t bcast[UG_MAX_T];     /* constant read in a per-image operand slot: replicated per image */
     uint32_t capacity, last_images;
     UQKSpatial sp[UG_MAX_OP];
     uint64_t ticks[UG_MAX_OP + 2];
@@ -438,7 +439,8 @@ static int validate(const uint8_t *p, uint32_t len)
 static int supported(uint32_t code)
 {
     switch (code) {
-    case 5: case 14: case 15: case 16: case 18: case 19: case 20: case 21: case 22: case 23: case 24: case 26: return 1;
+    case 5: case 10: case 14: case 15: case 16: case 18: case 19: case 20: case 21: case 22: case 23: case 24:
+    case 25: case 26: case 27: case 28: return 1;
     default: return 0;
     }
 }
@@ -693,6 +695,16 @@ int ug_load(const void *blob, uint32_t len)
     if (rc) return rc;
     for (uint32_t i = 0; i < G.h.no; i++)
         if (!supported(G.ops[i].code)) return 19;
+    /* Operands read image by image (every `a` except a pack list head, and
+     * the `b` of add, concat, mul and bmm). The loader lets a constant fill
+     * such a slot; it then gets one copy per image so that every kernel can
+     * step through stacked images uniformly. */
+    memset(G.bcast, 0, sizeof G.bcast);
+    for (uint32_t i = 0; i < G.h.no; i++) {
+        const Op *o = G.ops + i;
+        if (o->code != 19 && G.ts[o->a].flags) G.bcast[o->a] = 1;
+        if ((o->code == 18 || o->code == 20 || o->code == 25 || o->code == 27) && G.ts[o->b].flags) G.bcast[o->b] = 1;
+    }
     free(G.arena);
     G.arena = malloc(G.h.arena_bytes);
     if (!G.arena) return 24;
@@ -722,9 +734,12 @@ static int ensure_capacity(uint32_t images)
     }
     G.capacity = 0;
     for (uint32_t t = 0; t < G.h.nt; t++) {
-        if (G.ts[t].flags) continue;
+        if (G.ts[t].flags && !G.bcast[t]) continue;
         G.act[t] = uqk_malloc((size_t)images * G.ts[t].bytes);
         if (!G.act[t]) return 24;
+        if (G.ts[t].flags)
+            for (uint32_t k = 0; k < images; k++)
+                if (uqk_d2d(G.act[t] + (size_t)k * G.ts[t].bytes, G.dev_arena + G.ts[t].offset, G.ts[t].bytes)) return 24;
     }
     G.capacity = images;
     return 0;
@@ -764,6 +779,18 @@ static int enqueue_ops(uint32_t images)
             else rc = uqk_d2d(zp, ap, (size_t)images * z->bytes);
             break;
         case 22: rc = uqk_lut(ap, zp, (uint64_t)images * a->bytes, bp, a->type == 3 ? 128u : 0u); break;
+        case 10: rc = uqk_permute(ap, zp, images, a->rank, a->d, o->p, width(a->type)); break;
+        case 25: rc = uqk_mul(ap, bp, zp, (uint64_t)images * z->bytes, (const int32_t *)(A + G.ts[o->p[0]].offset)); break;
+        case 27: {
+            const int32_t *q = (const int32_t *)(A + G.ts[o->p[0]].offset);
+            rc = uqk_bmm(ap, bp, zp, images, z->d[0], z->d[1], z->d[2], a->d[q[5] ? 1 : 2], q);
+            break;
+        }
+        case 28: {
+            const uint32_t w = a->d[a->rank - 1];
+            rc = uqk_softmax(ap, zp, (uint64_t)images * (z->bytes / w), w, G.dev_arena + b->offset + 4);
+            break;
+        }
         case 20: {
             uint64_t outer = images, inner = 1;
             uint32_t axis = o->p[0];
@@ -818,7 +845,7 @@ static int enqueue_ops(uint32_t images)
 static void bind_pointers(const void *d_in, void *d_out)
 {
     for (uint32_t t = 0; t < G.h.nt; t++)
-        G.ptr[t] = G.ts[t].flags ? G.dev_arena + G.ts[t].offset : G.act[t];
+        G.ptr[t] = G.ts[t].flags && !G.bcast[t] ? G.dev_arena + G.ts[t].offset : G.act[t];
     if (d_in) G.ptr[G.h.input] = (uint8_t *)d_in;
     if (d_out && G.h.output != G.h.input && !G.ts[G.h.output].flags) G.ptr[G.h.output] = (uint8_t *)d_out;
 }

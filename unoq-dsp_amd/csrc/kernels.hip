@@ -1042,6 +1042,225 @@ extern "C" int uqk_window4(const void *x, void *y, uint32_t images, const uint32
 }
 
 // ---------------------------------------------------------------------------
+// Permutation (code 10, graph.c:374-390) of rank <= 4 tensors, per image:
+// out[i0,i1,i2,i3] = in[sum_d i_d * src_stride[d]], elements of 1 or 4 bytes.
+// ---------------------------------------------------------------------------
+struct Perm4 {
+    uint32_t out[4];
+    uint32_t src_stride[4];
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_permute(const T *x, T *y, uint64_t total, uint32_t count, Perm4 g)
+{
+    const uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= total) return;
+    const uint64_t img = idx / count;
+    uint32_t r = (uint32_t)(idx - img * count), src = 0;
+#pragma unroll
+    for (int d = 3; d >= 0; d--) {
+        const uint32_t o = r % g.out[d];
+        r /= g.out[d];
+        src += o * g.src_stride[d];
+    }
+    y[idx] = x[img * count + src];
+}
+
+extern "C" int uqk_permute(const void *x, void *y, uint32_t images, uint32_t rank, const uint32_t in_dims[4],
+                           const uint32_t perm[4], uint32_t elem_bytes)
+{
+    Perm4 g;
+    uint32_t stride[4] = {1, 1, 1, 1}, acc = 1, count = 1;
+    for (int d = (int)rank - 1; d >= 0; d--) {
+        stride[d] = acc;
+        acc *= in_dims[d];
+    }
+    // Leading unit dimensions pad the permutation to rank 4.
+    const uint32_t lead = 4 - rank;
+    for (uint32_t d = 0; d < 4; d++) {
+        g.out[d] = d < lead ? 1 : in_dims[perm[d - lead]];
+        g.src_stride[d] = d < lead ? 0 : stride[perm[d - lead]];
+        count *= g.out[d];
+    }
+    const uint64_t total = (uint64_t)count * images;
+    if (!total) return 0;
+    dim3 grid((unsigned)((total + 255) / 256));
+    if (elem_bytes == 4)
+        hipLaunchKernelGGL(k_permute<uint32_t>, grid, dim3(256), 0, g_stream, (const uint32_t *)x, (uint32_t *)y, total, count, g);
+    else
+        hipLaunchKernelGGL(k_permute<uint8_t>, grid, dim3(256), 0, g_stream, (const uint8_t *)x, (uint8_t *)y, total, count, g);
+    UQK_LAUNCHED();
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Elementwise product (uq_mul, qnn.c:111-116), 16 bytes per thread.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_mul(const int8_t *a, const int8_t *b, int8_t *y, uint64_t count,
+                                              int az, int bz, int yz, int m, int s, int lo, int hi)
+{
+    const uint64_t i0 = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 16;
+    if (i0 >= count) return;
+    if (i0 + 16 <= count) {
+        const v4i va = *(const v4i *)(a + i0), vb = *(const v4i *)(b + i0);
+        int w[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            int word = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int prod = (sbyte(va[q], j) - az) * (sbyte(vb[q], j) - bz);
+                const int v = min(max(uq_scale(prod, m, s) + yz, lo), hi);
+                word |= (v & 0xff) << (8 * j);
+            }
+            w[q] = word;
+        }
+        *(v4i *)(y + i0) = (v4i){w[0], w[1], w[2], w[3]};
+    } else {
+        for (uint64_t i = i0; i < count; i++) {
+            const int prod = ((int)a[i] - az) * ((int)b[i] - bz);
+            y[i] = (int8_t)min(max(uq_scale(prod, m, s) + yz, lo), hi);
+        }
+    }
+}
+
+extern "C" int uqk_mul(const void *a, const void *b, void *y, uint64_t count, const int32_t q[7])
+{
+    if (!count) return 0;
+    const uint64_t threads = (count + 15) / 16;
+    hipLaunchKernelGGL(k_mul, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, g_stream,
+                       (const int8_t *)a, (const int8_t *)b, (int8_t *)y, count, q[0], q[1], q[2], q[3], q[4], q[5], q[6]);
+    UQK_LAUNCHED();
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Batched int8 matmul (uq_bmm, qnn.c:117-153): z[h][r][c] =
+// clamp(scale(sum_t (A[h][r][t] - az) * (B[h][t][c] - bz)) + yz). The sum is
+// formed exactly in int32 (the loader bounds k * 255^2 * 2^max(s,0)).
+// One 256-thread block per 32x32 output tile; K in slices of 32 staged in LDS
+// as zero-point-shifted ints; each thread owns 4 rows of one column.
+// ---------------------------------------------------------------------------
+#define BMM_T 32
+__global__ __launch_bounds__(256) void k_bmm(const int8_t *A, const int8_t *B, int8_t *Z, uint32_t m, uint32_t n,
+                                              uint32_t k, uint32_t tiles_m, uint32_t tiles_n, uint32_t batches,
+                                              uint64_t b_image_stride, int ta, int tb, int az, int bz, int yz,
+                                              int mq, int s)
+{
+    __shared__ int As[BMM_T][BMM_T + 1], Bs[BMM_T][BMM_T + 1];
+    uint32_t blk = blockIdx.x;
+    const uint32_t tn = blk % tiles_n;
+    blk /= tiles_n;
+    const uint32_t tm = blk % tiles_m;
+    const uint32_t mat = blk / tiles_m;           // image * batches + h
+    const uint32_t img = mat / batches, h = mat - img * batches;
+    const int8_t *a = A + (uint64_t)mat * m * k;
+    const int8_t *b = B + img * b_image_stride + (uint64_t)h * k * n;
+    const uint32_t row0 = tm * BMM_T, col0 = tn * BMM_T;
+    const uint32_t tid = threadIdx.x, tx = tid & 31, ty = tid >> 5;
+    int acc[4] = {0, 0, 0, 0};
+    for (uint32_t k0 = 0; k0 < k; k0 += BMM_T) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t e = tid + 256 * j, hi = e >> 5, lo = e & 31;
+            // A tile element (r, t): lanes walk the contiguous axis in memory.
+            const uint32_t ra = ta ? lo : hi, ka = ta ? hi : lo;
+            const uint32_t r = row0 + ra, t = k0 + ka;
+            As[ra][ka] = (r < m && t < k) ? (int)a[ta ? (uint64_t)t * m + r : (uint64_t)r * k + t] - az : 0;
+            const uint32_t tb_ = tb ? lo : hi, cb = tb ? hi : lo;
+            const uint32_t c = col0 + cb, t2 = k0 + tb_;
+            Bs[tb_][cb] = (c < n && t2 < k) ? (int)b[tb ? (uint64_t)c * k + t2 : (uint64_t)t2 * n + c] - bz : 0;
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (int kk = 0; kk < BMM_T; kk++) {
+            const int bv = Bs[kk][tx];
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] += As[ty * 4 + i][kk] * bv;
+        }
+        __syncthreads();
+    }
+    const uint32_t c = col0 + tx;
+    if (c >= n) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t r = row0 + ty * 4 + i;
+        if (r < m) Z[((uint64_t)mat * m + r) * n + c] = (int8_t)min(max(uq_scale(acc[i], mq, s) + yz, -128), 127);
+    }
+}
+
+extern "C" int uqk_bmm(const void *a, const void *b, void *z, uint32_t images, uint32_t batches, uint32_t m,
+                       uint32_t n, uint32_t k, const int32_t q[7])
+{
+    const uint32_t tiles_m = (m + BMM_T - 1) / BMM_T, tiles_n = (n + BMM_T - 1) / BMM_T;
+    const uint64_t blocks = (uint64_t)tiles_m * tiles_n * batches * images;
+    if (!blocks) return 0;
+    if (blocks > 0x7fffffffULL) return (int)hipErrorInvalidValue;
+    const uint64_t b_stride = (uint64_t)batches * k * n;
+    hipLaunchKernelGGL(k_bmm, dim3((unsigned)blocks), dim3(256), 0, g_stream, (const int8_t *)a, (const int8_t *)b,
+                       (int8_t *)z, m, n, k, tiles_m, tiles_n, batches, b_stride, q[5], q[6], q[0], q[1], q[2], q[3], q[4]);
+    UQK_LAUNCHED();
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Exact int8 softmax (uq_softmax_exact, qnn.c:87-107): one wave per row.
+// Row max and the Q12 sum of table exponentials are wave reductions; every
+// lane then forms the same fixed-point reciprocal (three Newton-Raphson steps
+// on the sum normalised to [1, 2)) and writes its own elements.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int high_mul(int a, int b)
+{
+    return (int)(((long long)a * (long long)b + (1LL << 30)) >> 31);
+}
+
+__global__ __launch_bounds__(256) void k_softmax(const int8_t *x, int8_t *y, uint64_t rows, uint32_t width,
+                                                  const int *table)
+{
+    __shared__ int lut[256];
+    lut[threadIdx.x] = table[threadIdx.x];
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63;
+    const uint64_t row = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int8_t *src = x + row * width;
+    int mx = -128;
+    for (uint32_t j = lane; j < width; j += 64) mx = max(mx, (int)src[j]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = max(mx, __shfl_xor(mx, off, 64));
+    unsigned sum = 0;
+    for (uint32_t j = lane; j < width; j += 64) sum += ((unsigned)lut[mx - (int)src[j]] + 2048u) >> 12;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += (unsigned)__shfl_xor((int)sum, off, 64);
+    const unsigned lead = (unsigned)__clz((int)sum), exponent = 35 - lead;
+    const unsigned frac = (sum << lead) - 0x80000000u;
+    const int half = (int)(((unsigned long long)frac + 0x80000000ull) >> 1);
+    int r = 1515870810 + high_mul(half, -1010580540);
+#pragma unroll
+    for (int it = 0; it < 3; it++) {
+        const int err = 536870912 - high_mul(half, r);
+        r += high_mul(r, err) * 4;
+    }
+    const long long r2 = (long long)r * 2;
+    r = r2 > 2147483647LL ? 2147483647 : (int)r2;
+    int8_t *dst = y + row * width;
+    for (uint32_t j = lane; j < width; j += 64) {
+        const unsigned v = (unsigned)high_mul(r, lut[mx - (int)src[j]]);
+        const unsigned rounded = exponent >= 32 ? 0u : (v + (1u << (exponent - 1))) >> exponent;
+        dst[j] = (int8_t)(rounded > 255 ? 127 : (int)rounded - 128);
+    }
+}
+
+extern "C" int uqk_softmax(const void *x, void *y, uint64_t rows, uint32_t width, const void *table)
+{
+    if (!rows) return 0;
+    hipLaunchKernelGGL(k_softmax, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, g_stream, (const int8_t *)x,
+                       (int8_t *)y, rows, width, (const int *)table);
+    UQK_LAUNCHED();
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
 // Runtime plumbing.
 // ---------------------------------------------------------------------------
 extern "C" int uqk_device_count(void)

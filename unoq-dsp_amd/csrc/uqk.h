@@ -68,6 +68,18 @@ int uqk_resize(const void *x, void *y, uint32_t batches, uint32_t ih, uint32_t i
 int uqk_window4(const void *x, void *y, uint32_t images, const uint32_t in_dims[4], const uint32_t out_dims[4],
                 const int32_t offset[4], int32_t fill);
 
+/* Permutation (code 10) of a rank <= 4 tensor per image; z.d[i] = in_dims[perm[i]]. */
+int uqk_permute(const void *x, void *y, uint32_t images, uint32_t rank, const uint32_t in_dims[4],
+                const uint32_t perm[4], uint32_t elem_bytes);
+/* Elementwise product (code 25), q = {az, bz, yz, m, shift, lo, hi}. */
+int uqk_mul(const void *a, const void *b, void *y, uint64_t count, const int32_t q[7]);
+/* Batched matmul (code 27) of images * batches matrices, a [m][k] ([k][m]
+ * when q[5]), b [k][n] ([n][k] when q[6]), q = {az, bz, yz, m, shift, q5, q6}. */
+int uqk_bmm(const void *a, const void *b, void *z, uint32_t images, uint32_t batches, uint32_t m, uint32_t n,
+            uint32_t k, const int32_t q[7]);
+/* Exact softmax (code 28) over rows of `width` bytes; table = 256 Q0.31 exponentials. */
+int uqk_softmax(const void *x, void *y, uint64_t rows, uint32_t width, const void *table);
+
 /* Timing: a pool of HIP events recorded on the library stream. */
 int uqk_events(uint32_t count);
 int uqk_record(uint32_t index);

@@ -392,6 +392,70 @@ class Plan:
         self._op(19, ids[0], lt, z)
         return z
 
+    def transpose(self, x, perm):
+        """Code 10: permutation of any rank (graph.c:374-390), z.d[i] = x.d[perm[i]]."""
+        s = self.shape(x)
+        z = self.tensor([s[d] for d in perm], self.tensors[x]["type"])
+        self.zp[z] = self.zp.get(x, 0)
+        self._op(10, x, x, z, tuple(list(perm) + [0] * (4 - len(perm))))
+        return z
+
+    def _product_requant(self, rng, k, yz):
+        """Multiplier / shift for a sum of k products of zero-point-shifted int8
+        values, spreading the result over ~48 codes; respects the loader's
+        k * 255^2 * 2^max(shift, 0) <= 2147483520 bound (graph.c:189)."""
+        m = int(rng.multipliers(1)[0])
+        s = int(np.ceil(np.log2(48.0 / (np.sqrt(k) * 74.0 * 74.0)))) + int(rng.integers(1, -1, 1)[0])
+        s = max(-31, min(s, 15))
+        while k * 65025 * (1 << max(s, 0)) > 2147483520:
+            s -= 1
+        return m, s
+
+    def mul(self, a, b, act="none", yz=None):
+        """Code 25: elementwise product (qnn.c:111-116), q = [az, bz, yz, m, shift, lo, hi]."""
+        rng = self.rng()
+        yz = int(rng.integers(1, -128, 127)[0]) if yz is None else yz
+        m, s = self._product_requant(rng, 1, yz)
+        lo, hi = clamp_range(act, yz)
+        qt = self.tensor((7,), TYPE_I32, [self.zp[a], self.zp[b], yz, m, s, lo, hi])
+        z = self.tensor(self.shape(a))
+        self.zp[z] = yz
+        self._op(25, a, b, z, (qt, 0, 0, 0))
+        return z
+
+    def bmm(self, a, b, trans_a=False, trans_b=False, yz=None):
+        """Code 27: batched int8 matmul of rank-3 tensors (qnn.c:117-153).
+        a is [B][M][K] ([B][K][M] when trans_a), b is [B][K][N] ([B][N][K]
+        when trans_b); q = [az, bz, yz, m, shift, trans_a, trans_b]."""
+        sa, sb = self.shape(a), self.shape(b)
+        mm, k = (sa[2], sa[1]) if trans_a else (sa[1], sa[2])
+        n = sb[1] if trans_b else sb[2]
+        assert (sb[2] if trans_b else sb[1]) == k and sa[0] == sb[0]
+        rng = self.rng()
+        yz = int(rng.integers(1, -128, 127)[0]) if yz is None else yz
+        m, s = self._product_requant(rng, k, yz)
+        qt = self.tensor((7,), TYPE_I32, [self.zp[a], self.zp[b], yz, m, s, int(trans_a), int(trans_b)])
+        z = self.tensor((sa[0], mm, n))
+        self.zp[z] = yz
+        self._op(27, a, b, z, (qt, 0, 0, 0))
+        self.macs += sa[0] * mm * n * k
+        return z
+
+    def softmax(self, x, beta_scale=None):
+        """Code 28: exact int8 softmax over the last axis (qnn.c:87-107) with a
+        257-entry table: width, then Q0.31 exp(-d * beta_scale) for d = 0..255."""
+        rng = self.rng()
+        if beta_scale is None:
+            beta_scale = float(0.01 + 0.3 * rng.uniform01(1)[0])
+        d = np.arange(256, dtype=np.float64)
+        table = np.minimum(np.round(np.exp(-d * beta_scale) * 2.0 ** 31), 2147483647).astype(np.int64)
+        table[0] = 2147483647
+        bt = self.tensor((257,), TYPE_I32, np.concatenate(([self.shape(x)[-1]], table)))
+        z = self.tensor(self.shape(x))
+        self.zp[z] = -128
+        self._op(28, x, bt, z)
+        return z
+
     # -- serialisation -----------------------------------------------------
     def build(self, output, version=2):
         hdr = struct.pack("<8I", MAGIC, version, len(self.tensors), len(self.ops), len(self.arena),
