@@ -571,6 +571,26 @@ static void epilogue_record(int32_t *e, int64_t bias, int32_t m, int32_t shift)
     memcpy(e + 6, &cthr, 8);
 }
 
+/* The conv record of layers whose every shift is in [-22, -1] (T in
+ * [32, 53]): c1 also absorbs the corrected bias times m and the output zero
+ * point times 2^T, so the kernel's one multiply-add gives the whole affine
+ * value q = (acc + bias) * m + c1 + yz * 2^T. Summed mod 2^64: q itself fits
+ * in int64 (|v * m| < 2^62, c1 <= 2^30 + 2^52, |yz * 2^T| <= 2^60) and the
+ * multiply-add is exact mod 2^64. cthr moves by the same yz * 2^T. */
+static void epilogue_record_hi(int32_t *e, int64_t bias, int32_t m, int32_t shift, int32_t yz)
+{
+    int n = -shift, T = 31 + n;
+    uint64_t c1 = ((uint64_t)1 << 30) + ((uint64_t)1 << (30 + n)) + (uint64_t)bias * (uint64_t)(int64_t)m +
+                  ((uint64_t)(int64_t)yz << T);
+    int64_t cthr = ((int64_t)1 << (30 + n)) + (int64_t)yz * ((int64_t)1 << T);
+    e[0] = (int32_t)(uint32_t)(uint64_t)bias;
+    e[1] = m;
+    e[2] = 0;
+    e[3] = T;
+    memcpy(e + 4, &c1, 8);
+    memcpy(e + 6, &cthr, 8);
+}
+
 /* Build one spatial op's descriptor and host-side tables (graph-time work of
  * the reference's prepare step, qnn.c:388-501, re-targeted at the GPU). */
 static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
@@ -591,6 +611,9 @@ static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
     if (o->code != 16 && o->p[1]) d->lut = G.dev_arena + G.ts[o->p[1] - 1].offset;
     const int oc = q[17];
     const int32_t *bias = q + UQ_HEAD, *mult = bias + oc, *shift = mult + oc;
+    d->hi_shift = o->code == 14;
+    for (int c = 0; c < oc; c++)
+        if (shift[c] > -1 || shift[c] < -22) d->hi_shift = 0;
     const int8_t *w = (const int8_t *)(G.arena + G.ts[o->b].offset);
     if (o->code == 14) {
         ConvPlan cp = conv_plan(o);
@@ -612,7 +635,8 @@ static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
             }
             /* u = s + 128 on every column; the K tail holds xz + 128. */
             int64_t b2 = (int64_t)bias[n] + 128 * all + (int64_t)q[12] * tail;
-            epilogue_record(epi + 8 * n, b2, mult[n], shift[n]);
+            if (d->hi_shift) epilogue_record_hi(epi + 8 * n, b2, mult[n], shift[n], q[13]);
+            else epilogue_record(epi + 8 * n, b2, mult[n], shift[n]);
         }
         if (cp.mode == UQK_ROWS16 || cp.mode == UQK_ROWS4) {
             /* Slice -> byte offset inside the LDS row tile (full-width rows,

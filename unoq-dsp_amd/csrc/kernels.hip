@@ -110,7 +110,7 @@ struct ConvArgs {
     const int *delta;
     const uint8_t *lut;
     long M;
-    int ih, iw, ic, icp, oh, ow, oc, kh, sh, sw, dh, pt, pl, xz, yz, lo, hi, K, kpad, ohw, corr;
+    int ih, iw, ic, icp, oh, ow, oc, kh, sh, sw, dh, pt, pl, xz, yz, lo, hi, K, kpad, ohw, corr, emode;
     int tiles, cols, rows_max;
 };
 
@@ -162,13 +162,8 @@ __device__ __forceinline__ v4i gather16(const ConvArgs &a, const int8_t *base, i
     }
 }
 
-// Requantise a wave's RB*16 x NT*16 tile and store the valid rows
-// [row_base, row_limit). The MFMA result gives a lane one channel (lane & 15)
-// of four consecutive rows; the four bytes are packed into a word, and a 4x4
-// byte transpose across each quad of lanes (two DPP quad permutes, two
-// v_perm) turns that into one row x four channels per lane, stored as one
-// dword. Needs OC % 4 == 0 (so a quad's channels are all valid or all not);
-// other widths take byte stores.
+// 4x4 byte transpose across a quad of lanes: lane j of the quad ends with
+// byte j of each of the four lanes' words.
 __device__ __forceinline__ int quad_transpose_bytes(int w, int lane)
 {
     const int j = lane & 3;
@@ -185,26 +180,78 @@ __device__ __forceinline__ int pack4(int v0, int v1, int v2, int v3)
     return (int)(lo | hi);
 }
 
-template <int RB, int NT>
+// Clamp to [lo, hi] in one v_med3_i32 (the compiler keeps min/max apart).
+__device__ __forceinline__ int med3(int x, int lo, int hi)
+{
+    int r;
+    asm("v_med3_i32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(lo), "v"(hi));
+    return r;
+}
+
+// Conv requantisation of an MFMA accumulator.
+// HI (layers whose every channel has shift in [-22, -1]): the record's c1
+// already holds corrected_bias * m + yz * 2^T (computed mod 2^64 at load
+// time), so q = acc * m + c1 is the full affine value; T >= 32 makes q >> T
+// the high word of q (or of the corrected q - 2^31) shifted by T - 32.
+// Generic: v = (acc + bias) << ls, q = v * m + c1, then the zero point.
+// CORR: the clamp lets negative values through (act_min < output zero point).
+template <bool HI, bool CORR>
+__device__ __forceinline__ int conv_requant(int acc, const Epi &e, int yz, int lo, int hi)
+{
+    if (HI) {
+        const long long q = (long long)acc * (long long)e.m + e.c1;
+        int h = (int)(q >> 32);
+        if (CORR && q < e.cthr) h = (int)((q - (1LL << 31)) >> 32);
+        return med3(h >> (e.T - 32), lo, hi);
+    }
+    const int v = (int)(((unsigned)acc + (unsigned)e.bias) << e.ls);
+    long long q = (long long)v * (long long)e.m + e.c1;
+    if (CORR && q < e.cthr) q -= (1LL << 31);
+    return med3((int)(q >> e.T) + yz, lo, hi);
+}
+
+// Stage the block's per-channel records (columns n0 .. n0 + NT*16 - 1; the
+// channels past OC reuse record 0) and the layer's 256-byte post table in
+// LDS, so that the epilogue has no dependent global load. The caller's next
+// barrier publishes them.
+template <int NT>
+__device__ __forceinline__ void stage_consts(const ConvArgs &a, int n0, int4 *epi_s, int8_t *lut_s)
+{
+    for (int t = threadIdx.x; t < 2 * NT * 16; t += 256) {
+        const int col = n0 + (t >> 1);
+        epi_s[t] = a.epi[2 * (col < a.oc ? col : 0) + (t & 1)];
+    }
+    if (a.lut && threadIdx.x < 64) ((int *)lut_s)[threadIdx.x] = ((const int *)a.lut)[threadIdx.x];
+}
+
+// Requantise a wave's RB*16 x NT*16 tile and store the valid rows
+// [row_base, row_limit). The MFMA result gives a lane one channel (lane & 15)
+// of four consecutive rows; the four bytes are packed into a word, and a 4x4
+// byte transpose across each quad of lanes (two DPP quad permutes, two
+// v_perm) turns that into one row x four channels per lane, stored as one
+// dword. Needs OC % 4 == 0 (so a quad's channels are all valid or all not);
+// other widths take byte stores.
+template <int RB, int NT, bool HI, bool CORR>
 __device__ __forceinline__ void conv_store(const ConvArgs &a, const v4i (&acc)[RB][NT], int8_t *stage, int n0, int lane,
-                                           long row_base, long row_limit)
+                                           long row_base, long row_limit, const int4 *epi_s, const int8_t *lut_s)
 {
     constexpr int R = RB * 16;
     constexpr int BN = NT * 16;
     constexpr int STRIDE = BN + 16;
     const int lr = lane & 15, lg = lane >> 4;
     const bool words = (a.oc & 3) == 0;
+    const bool lut = a.lut != nullptr;
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
-        const int col = n0 + nt * 16 + lr;
-        const Epi e = load_epi(a.epi, col < a.oc ? col : 0);
+        const Epi e = load_epi(epi_s, nt * 16 + lr);
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) {
             int v[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                v[i] = uq_requant_affine(acc[rb][nt][i], e, a.corr, a.yz, a.lo, a.hi);
-                if (a.lut) v[i] = (int)(signed char)a.lut[v[i] + 128];
+            for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[rb][nt][i], e, a.yz, a.lo, a.hi);
+            if (lut) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = lut_s[v[i] + 128];
             }
             if (words) {
                 const int t = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
@@ -234,12 +281,28 @@ __device__ __forceinline__ void conv_store(const ConvArgs &a, const v4i (&acc)[R
     }
 }
 
+// One copy of the store per requantisation variant (emode = HI | CORR << 1).
+template <int RB, int NT>
+__device__ __forceinline__ void conv_epilogue(const ConvArgs &a, const v4i (&acc)[RB][NT], int8_t *stage, int n0,
+                                              int lane, long row_base, long row_limit, const int4 *epi_s,
+                                              const int8_t *lut_s)
+{
+    switch (a.emode) {
+    case 0: conv_store<RB, NT, false, false>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s); break;
+    case 1: conv_store<RB, NT, true, false>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s); break;
+    case 2: conv_store<RB, NT, false, true>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s); break;
+    default: conv_store<RB, NT, true, true>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s); break;
+    }
+}
+
 template <int RB, int NT, int MODE>
 __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
 {
     constexpr int R = RB * 16;
     constexpr int STRIDE = NT * 16 + 16;
     __shared__ __attribute__((aligned(16))) int8_t stage[4][R * STRIDE];
+    __shared__ __attribute__((aligned(4))) int8_t lut_s[256];
+    __shared__ int4 epi_s[2 * NT * 16];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;
@@ -268,12 +331,6 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
         }
     }
 
-    v4i acc[RB][NT];
-#pragma unroll
-    for (int rb = 0; rb < RB; rb++)
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) acc[rb][nt] = (v4i){0, 0, 0, 0};
-
     const int8_t *wrow = a.w + (long)(n0 + lr) * a.kpad + lg * 16;
     const int steps = a.kpad >> 6;
     v4i A[RB], B[NT];
@@ -281,6 +338,12 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
     for (int rb = 0; rb < RB; rb++) A[rb] = gather16<MODE>(a, base[rb], iy0[rb], ix0[rb], valid[rb], lg * 16, xzw);
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) B[nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad);
+    stage_consts<NT>(a, n0, epi_s, lut_s);
+    v4i acc[RB][NT];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[rb][nt] = (v4i){0, 0, 0, 0};
     for (int s = 0; s < steps; s++) {
         v4i An[RB], Bn[NT];
         const bool more = s + 1 < steps;
@@ -303,7 +366,8 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
             for (int nt = 0; nt < NT; nt++) B[nt] = Bn[nt];
         }
     }
-    conv_store<RB, NT>(a, acc, stage[wave], n0, lane, row0, a.M);
+    __syncthreads();
+    conv_epilogue<RB, NT>(a, acc, stage[wave], n0, lane, row0, a.M, epi_s, lut_s);
 }
 
 // Spatial conv with the block's input rows staged in LDS. A block covers BM =
@@ -319,6 +383,8 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
     constexpr int R = RB * 16;
     constexpr int BM = 4 * R;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    __shared__ __attribute__((aligned(4))) int8_t lut_s[256];
+    __shared__ int4 epi_s[2 * NT * 16];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;
@@ -374,6 +440,7 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
         }
     }
     for (int i = threadIdx.x; i < ndelta; i += 256) dl[i] = a.delta[i];
+    stage_consts<NT>(a, n0, epi_s, lut_s);
     __syncthreads();
 
     int lbase[RB];
@@ -387,17 +454,16 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
         lbase[rb] = ((oy - oy_a) * a.sh * a.cols + ox * a.sw) * a.icp;
     }
 
-    v4i acc[RB][NT];
-#pragma unroll
-    for (int rb = 0; rb < RB; rb++)
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) acc[rb][nt] = (v4i){0, 0, 0, 0};
-
     const int8_t *wrow = a.w + (long)(n0 + lr) * a.kpad + lg * 16;
     const int steps = a.kpad >> 6;
     v4i B[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) B[nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad);
+    v4i acc[RB][NT];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[rb][nt] = (v4i){0, 0, 0, 0};
     for (int s = 0; s < steps; s++) {
         const int kg = s * 64 + lg * 16;
         v4i Bn[NT];
@@ -434,7 +500,7 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
         }
     }
     const long img0 = n * a.ohw;
-    conv_store<RB, NT>(a, acc, stage, n0, lane, img0 + p0 + wave * R, img0 + pend);
+    conv_epilogue<RB, NT>(a, acc, stage, n0, lane, img0 + p0 + wave * R, img0 + pend, epi_s, lut_s);
 }
 
 template <int RB, int NT>
@@ -507,6 +573,7 @@ extern "C" int uqk_conv(const UQKSpatial *d, const void *x, void *y, uint32_t ba
     a.kh = d->kh; a.sh = d->sh; a.sw = d->sw; a.dh = d->dh; a.pt = d->pt; a.pl = d->pl;
     a.xz = d->xz; a.yz = d->yz; a.lo = d->lo; a.hi = d->hi;
     a.K = d->K; a.kpad = d->kpad; a.ohw = d->oh * d->ow; a.corr = d->corr;
+    a.emode = (d->hi_shift ? 1 : 0) | (d->corr ? 2 : 0);
     a.cols = (d->ow - 1) * d->sw + (d->kw - 1) * d->dw + 1;
     if (a.M <= 0) return 0;
     const int nchunks = d->oc_pad / (16 * d->nt);

@@ -27,6 +27,7 @@ typedef struct {
     int32_t kh, kw, sh, sw, dh, dw, pt, pl;
     int32_t xz, yz, lo, hi;
     int32_t K, kpad, oc_pad, mode, nt, rb, is_max, vec, corr;
+    int32_t hi_shift;          /* conv, every shift in [-22, -1]: records fold bias and zero point into c1 */
     const void *w;
     const void *wdot;
     const void *epi;
