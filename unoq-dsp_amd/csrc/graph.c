@@ -539,10 +539,12 @@ static Layout spatial_layout(const Op *o, size_t at)
         L.kmap = align256(L.epi + (size_t)oc * 32);
         L.end = align256(L.kmap + (size_t)c.table_bytes);
     } else if (o->code == 15) {
-        int groups = (q[0] * q[1] + 3) / 4;
+        /* Tap words: (taps + 3) / 4 groups for k_dw_tile, kh * 2 rows of one
+         * or two words for k_dw_win; room for either. */
+        int groups = (q[0] * q[1] + 3) / 4, rows = 2 * q[0];
         L.epi = at;
         L.w = align256(L.epi + (size_t)oc * 32);
-        L.end = align256(L.w + (size_t)groups * oc * 4);
+        L.end = align256(L.w + (size_t)(groups > rows ? groups : rows) * oc * 4);
     }
     return L;
 }
@@ -611,7 +613,8 @@ static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
     if (o->code != 16 && o->p[1]) d->lut = G.dev_arena + G.ts[o->p[1] - 1].offset;
     const int oc = q[17];
     const int32_t *bias = q + UQ_HEAD, *mult = bias + oc, *shift = mult + oc;
-    d->hi_shift = o->code == 14;
+    d->dwwin = o->code == 15 && uqk_dw_win_lds(d) > 0;
+    d->hi_shift = o->code == 14 || d->dwwin;
     for (int c = 0; c < oc; c++)
         if (shift[c] > -1 || shift[c] < -22) d->hi_shift = 0;
     const int8_t *w = (const int8_t *)(G.arena + G.ts[o->b].offset);
@@ -664,14 +667,27 @@ static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
         int taps = q[0] * q[1], groups = (taps + 3) / 4;
         int32_t *epi = (int32_t *)(host_pool + L->epi);
         int8_t *wd = (int8_t *)host_pool + L->w;
+        const int kh = q[0], kw = q[1], nwk = kw > 4 ? 2 : 1;
         for (int c = 0; c < oc; c++) {
             int64_t all = 0;
             for (int t = 0; t < taps; t++) all += w[t * oc + c];
-            epilogue_record(epi + 8 * c, (int64_t)bias[c] + 128 * all, mult[c], shift[c]);
-            /* Four consecutive taps of one channel per 32-bit word, for dot4. */
-            for (int g = 0; g < groups; g++)
-                for (int j = 0; j < 4; j++)
-                    wd[((size_t)g * oc + c) * 4 + j] = 4 * g + j < taps ? w[(4 * g + j) * oc + c] : 0;
+            if (d->hi_shift) epilogue_record_hi(epi + 8 * c, (int64_t)bias[c] + 128 * all, mult[c], shift[c], q[13]);
+            else epilogue_record(epi + 8 * c, (int64_t)bias[c] + 128 * all, mult[c], shift[c]);
+            if (d->dwwin) {
+                /* Kernel row ky, word k: taps kx = 4k .. 4k + 3 of the row
+                 * (zero past kw), at [ky][k][C]. */
+                for (int ky = 0; ky < kh; ky++)
+                    for (int k = 0; k < nwk; k++)
+                        for (int j = 0; j < 4; j++) {
+                            int kx = 4 * k + j;
+                            wd[(((size_t)ky * nwk + k) * oc + c) * 4 + j] = kx < kw ? w[(ky * kw + kx) * oc + c] : 0;
+                        }
+            } else {
+                /* Four consecutive taps of one channel per 32-bit word, for dot4. */
+                for (int g = 0; g < groups; g++)
+                    for (int j = 0; j < 4; j++)
+                        wd[((size_t)g * oc + c) * 4 + j] = 4 * g + j < taps ? w[(4 * g + j) * oc + c] : 0;
+            }
         }
         d->w = G.dev_arena + G.ts[o->b].offset;
         d->wdot = G.dev_prep + L->w;

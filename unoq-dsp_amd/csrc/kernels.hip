@@ -586,14 +586,22 @@ extern "C" int uqk_conv(const UQKSpatial *d, const void *x, void *y, uint32_t ba
         if (rb == 4) launch_rows_nt<4>(d->nt, d->mode, a, grid, uqk_conv_rows_lds(d, rb));
         else launch_rows_nt<2>(d->nt, d->mode, a, grid, uqk_conv_rows_lds(d, rb));
     } else {
+        // Narrower channel slices when the batch gives too few waves to keep
+        // four per SIMD (1024 SIMDs): more slices re-read the (small) input
+        // but hide the K loop's load latency. 8 -> 4 -> 2 and 6 -> 2 keep
+        // oc_pad (a multiple of 16 * NT) a whole number of slices.
+        int nt = d->nt;
+        const long row_waves = (a.M + 15) / 16;
+        while (nt > 2 && row_waves * (d->oc_pad / (16 * nt)) < 4096) nt = nt == 8 ? 4 : 2;
+        const int chunks = d->oc_pad / (16 * nt);
         // Two row blocks per wave only when that still gives every SIMD of
         // the chip several waves.
-        const long waves2 = (a.M + 31) / 32 * nchunks;
+        const long waves2 = (a.M + 31) / 32 * chunks;
         const int rb = waves2 >= 8192 ? 2 : 1;
         const long rows = 4L * 16 * rb;
-        dim3 grid((unsigned)((a.M + rows - 1) / rows), (unsigned)nchunks);
-        if (rb == 2) launch_conv_nt<2>(d->nt, d->mode, a, grid, 0);
-        else launch_conv_nt<1>(d->nt, d->mode, a, grid, 0);
+        dim3 grid((unsigned)((a.M + rows - 1) / rows), (unsigned)chunks);
+        if (rb == 2) launch_conv_nt<2>(nt, d->mode, a, grid, 0);
+        else launch_conv_nt<1>(nt, d->mode, a, grid, 0);
     }
     UQK_LAUNCHED();
     return 0;
@@ -815,6 +823,247 @@ __global__ __launch_bounds__(256) void k_dw_tile(DwTileArgs a)
     }
 }
 
+// Depthwise 3x3 / 5x5, stride 1 or 2, no dilation, C % 4 == 0, on tap
+// windows. A block covers TH output rows x 4*XW output columns x 4*CQ
+// channels of one image. Its input rows are staged in LDS as windows: the
+// word W[r][j][c] holds channel c of the four input columns S*j .. S*j + 3 of
+// staged row r, so output column x (tile-relative) finds its first four taps
+// of row r in window j = x and, for 5x5, its fifth tap in byte 0 of window
+// x + 4/S. Windows are laid out [row][j / 4][channel % 4][channel / 4][j % 4]
+// with CQ * 16 bytes of padding after each j / 4 block: a thread's four
+// consecutive output columns of one channel are one 16-byte LDS read,
+// neighbouring lanes (neighbouring channel quads) read neighbouring 16-byte
+// blocks, and the padded stride (80 * CQ bytes) spreads the lanes of
+// different column quads over distinct banks. Each
+// thread computes 4 columns x 4 channels; per kernel row and channel that is
+// four v_dot4 against the row's taps packed in a word (a zero weight on the
+// unused lane of the word). The windows are built from the input rows with a
+// 4x4 byte transpose (channel-major words of four columns) and v_alignbyte
+// for the shifted starts. Requantisation uses the conv epilogue's records.
+struct DwWinArgs {
+    const int8_t *x;
+    int8_t *y;
+    const int4 *wrow;          // [ky][wk][C] words of four taps (C/4 int4 per row)
+    const int4 *epi;
+    const uint8_t *lut;
+    int ih, iw, c, oh, ow, pt, pl, xz, yz, lo, hi;
+    int th, xw, cq, tiles_x, tiles, ir, njq;
+    int lcq;                   // log2(cq)
+    int njq_magic, xw_magic;   // ceil(2^16 / njq), ceil(2^16 / xw): exact small quotients
+};
+
+template <int KS, int S, bool HI, bool CORR>
+__global__ __launch_bounds__(256) void k_dw_win(DwWinArgs a)
+{
+    constexpr int NWK = KS > 4 ? 2 : 1;
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    int *W = (int *)smem;
+    const int cb = 4 * a.cq;
+    // LDS: windows | tap words [ky][wk][cb] | channel records [cb][2] | table
+    const int jqs = 5 * cb;   // dwords per j / 4 block: 4 * cb data + 4 * cq padding
+    int *wt = (int *)(smem + (size_t)a.ir * a.njq * jqs * 4);
+    int4 *et = (int4 *)(wt + KS * NWK * cb);
+    int8_t *lut_s = (int8_t *)(et + 2 * cb);
+    const long n = blockIdx.x / a.tiles;
+    const int tile = (int)(blockIdx.x - n * a.tiles);
+    const int ty = tile / a.tiles_x, tx = tile - ty * a.tiles_x;
+    const int c0 = blockIdx.y * cb;
+    const int oy0 = ty * a.th, ox0 = tx * 4 * a.xw;
+    const int iy0 = oy0 * S - a.pt, ix0 = ox0 * S - a.pl;
+    const int8_t *xim = a.x + n * a.ih * a.iw * a.c + c0;
+    const int xzw = (a.xz & 0xff) * 0x01010101;
+
+    // This thread's output item: 4 columns x 4 channels.
+    const int tid = threadIdx.x;
+    const int cqi = tid & (a.cq - 1), rest = tid >> a.lcq;
+    const int tyi = (rest * a.xw_magic) >> 16, xq = rest - tyi * a.xw;
+    const bool live = tyi < a.th && oy0 + tyi < a.oh;
+    const int cbase = c0 + 4 * cqi;
+
+    // The block's tap words and channel records.
+    for (int u = tid; u < KS * NWK * a.cq; u += 256) {
+        const int row = u >> a.lcq, cqd = u & (a.cq - 1);
+        *(v4i *)(wt + row * cb + 4 * cqd) = *(const v4i *)(a.wrow + ((long)row * a.c + c0) / 4 + cqd);
+    }
+    // Records as [half][channel % 4][channel / 4] int4s: lanes read 16-byte steps.
+    for (int u = tid; u < 2 * cb; u += 256) {
+        const int h = u >> (a.lcq + 2), rem = u & (cb - 1), i = rem >> a.lcq, cqd = rem & (a.cq - 1);
+        et[u] = a.epi[2 * (c0 + 4 * cqd + i) + h];
+    }
+
+    // Stage windows: one unit = 4 consecutive windows x 4 channels of a row.
+    const int units = a.ir * a.njq * a.cq;
+    for (int u = tid; u < units; u += 256) {
+        const int cqd = u & (a.cq - 1), r2 = u >> a.lcq;
+        const int r = (r2 * a.njq_magic) >> 16, jq = r2 - r * a.njq;
+        const int iy = iy0 + r;
+        const bool rowin = (unsigned)iy < (unsigned)a.ih;
+        const int8_t *src = xim + (rowin ? iy : 0) * a.iw * a.c + 4 * cqd;
+        const int px0 = ix0 + S * 4 * jq;
+        // Every load reads a valid pixel (padding positions re-read column 0)
+        // and the padding value is selected afterwards: no branches.
+        int P[4 * S + 4];
+#pragma unroll
+        for (int p = 0; p < 4 * S + 4; p++) {
+            const int ix = px0 + p;
+            const bool in = rowin && (unsigned)ix < (unsigned)a.iw;
+            const int v = *(const int *)(src + (in ? ix : 0) * a.c);
+            P[p] = in ? v : xzw;
+        }
+        int col[S + 1][4];   // col[g][i]: channel i over columns 4g .. 4g + 3
+#pragma unroll
+        for (int g = 0; g < S + 1; g++)
+            transpose4x4(P[4 * g], P[4 * g + 1], P[4 * g + 2], P[4 * g + 3], col[g][0], col[g][1], col[g][2], col[g][3]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int w4[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int start = S * t;              // first column of window 4*jq + t
+                const int g = start >> 2, sh = start & 3;
+                w4[t] = sh ? (int)__builtin_amdgcn_alignbyte((unsigned)col[g + 1][i], (unsigned)col[g][i], (unsigned)sh)
+                           : col[g][i];
+            }
+            *(v4i *)(W + ((long)r * a.njq + jq) * jqs + (i * a.cq + cqd) * 4) = (v4i){w4[0], w4[1], w4[2], w4[3]};
+        }
+    }
+    if (a.lut && tid < 64) ((int *)lut_s)[tid] = ((const int *)a.lut)[tid];
+    __syncthreads();
+    if (!live) return;
+
+    int acc[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[t][i] = 0;
+    // 5x5: one kernel row at a time keeps the register footprint small
+    // enough for several waves per SIMD.
+#pragma unroll (KS > 4 ? 1 : KS)
+    for (int ky = 0; ky < KS; ky++) {
+        const int r = tyi * S + ky;
+        const int *row = W + (long)r * a.njq * jqs + cqi * 4;
+        const v4i w0 = *(const v4i *)(wt + (ky * NWK) * cb + 4 * cqi);
+        const v4i w1 = *(const v4i *)(wt + (ky * NWK + NWK - 1) * cb + 4 * cqi);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const v4i win = *(const v4i *)(row + (long)xq * jqs + i * a.cq * 4);
+#pragma unroll
+            for (int t = 0; t < 4; t++) acc[t][i] = __builtin_amdgcn_sdot4(win[t], w0[i], acc[t][i], false);
+            if (KS > 4) {
+                int w2[4];
+                if (S == 1) {
+                    const v4i v = *(const v4i *)(row + (long)(xq + 1) * jqs + i * a.cq * 4);
+                    w2[0] = v[0]; w2[1] = v[1]; w2[2] = v[2]; w2[3] = v[3];
+                } else {
+                    const int2 lo2 = *(const int2 *)(row + (long)xq * jqs + i * a.cq * 4 + 2);
+                    const int2 hi2 = *(const int2 *)(row + (long)(xq + 1) * jqs + i * a.cq * 4);
+                    w2[0] = lo2.x; w2[1] = lo2.y; w2[2] = hi2.x; w2[3] = hi2.y;
+                }
+#pragma unroll
+                for (int t = 0; t < 4; t++) acc[t][i] = __builtin_amdgcn_sdot4(w2[t], w1[i], acc[t][i], false);
+            }
+        }
+    }
+    const int oy = oy0 + tyi;
+    int8_t *yrow = a.y + ((n * a.oh + oy) * a.ow) * (long)a.c + cbase;
+    Epi e[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int4 lo4 = et[i * a.cq + cqi], hi4 = et[cb + i * a.cq + cqi];
+        e[i].bias = lo4.x; e[i].m = lo4.y; e[i].ls = lo4.z; e[i].T = lo4.w;
+        e[i].c1 = (long long)(((unsigned long long)(unsigned)hi4.y << 32) | (unsigned)hi4.x);
+        e[i].cthr = (long long)(((unsigned long long)(unsigned)hi4.w << 32) | (unsigned)hi4.z);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int ox = ox0 + 4 * xq + t;
+        if (ox >= a.ow) break;
+        int v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[t][i], e[i], a.yz, a.lo, a.hi);
+        if (a.lut) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = lut_s[v[i] + 128];
+        }
+        *(int *)(yrow + (long)ox * a.c) = pack4(v[0], v[1], v[2], v[3]);
+    }
+}
+
+// Tile geometry for k_dw_win; returns the dynamic LDS bytes, 0 if unsuited.
+static size_t dw_win_plan(const UQKSpatial *d, DwWinArgs *t)
+{
+    const int ks = d->kh, s = d->sh;
+    if (d->oc % 4 || d->kh != d->kw || (ks != 3 && ks != 5) || d->sh != d->sw || (s != 1 && s != 2) ||
+        d->dh != 1 || d->dw != 1)
+        return 0;
+    const int c4 = d->oc / 4;
+    int cq = 1;
+    while (cq < 16 && c4 % (2 * cq) == 0) cq *= 2;
+    const int xq_all = (d->ow + 3) / 4;
+    const int tiles_x = (xq_all + 7) / 8;
+    const int xw = (xq_all + tiles_x - 1) / tiles_x;
+    // Wide rows take four channel quads per block, narrow maps more.
+    if (xw >= 4 && cq > 4) cq = 4;
+    int th = 256 / (xw * cq);
+    if (th < 1) return 0;
+    if (th > d->oh) th = d->oh;
+    t->th = th; t->xw = xw; t->cq = cq; t->tiles_x = tiles_x;
+    t->ir = (th - 1) * s + ks;
+    const int nj = 4 * xw + (ks > 4 ? 4 / s : 0);
+    t->njq = (nj + 3) / 4;
+    t->lcq = 0;
+    while ((1 << t->lcq) < cq) t->lcq++;
+    // (v * ceil(2^16 / d)) >> 16 == v / d for v < 2^16 / d; here v < 256 / cq
+    // (items) and v < ir * njq (staging rows), both far below that bound.
+    t->njq_magic = (65536 + t->njq - 1) / t->njq;
+    t->xw_magic = (65536 + xw - 1) / xw;
+    if (t->ir * t->njq >= 65536 / t->njq) return 0;
+    const size_t bytes = (size_t)t->ir * t->njq * cq * 5 * 16 + (size_t)ks * (ks > 4 ? 2 : 1) * cq * 16 +
+                         (size_t)cq * 4 * 32 + 256;
+    return bytes <= 65536 ? bytes : 0;
+}
+
+extern "C" size_t uqk_dw_win_lds(const UQKSpatial *d)
+{
+    DwWinArgs t;
+    return dw_win_plan(d, &t);
+}
+
+static int launch_dw_win(const UQKSpatial *d, const void *x, void *y, uint32_t batches)
+{
+    DwWinArgs a;
+    const size_t lds = dw_win_plan(d, &a);
+    if (!lds) return -1;
+    a.x = (const int8_t *)x;
+    a.y = (int8_t *)y;
+    a.wrow = (const int4 *)d->wdot;
+    a.epi = (const int4 *)d->epi;
+    a.lut = (const uint8_t *)d->lut;
+    a.ih = d->ih; a.iw = d->iw; a.c = d->oc; a.oh = d->oh; a.ow = d->ow; a.pt = d->pt; a.pl = d->pl;
+    a.xz = d->xz; a.yz = d->yz; a.lo = d->lo; a.hi = d->hi;
+    a.tiles = (d->oh + a.th - 1) / a.th * a.tiles_x;
+    const unsigned long long blocks = (unsigned long long)a.tiles * batches;
+    if (blocks > 0x7fffffffULL) return -1;
+    dim3 grid((unsigned)blocks, (unsigned)(d->oc / (4 * a.cq)));
+    const int mode = (d->hi_shift ? 1 : 0) | (d->corr ? 2 : 0);
+#define UQK_DWW(K, S)                                                                                        \
+    do {                                                                                                     \
+        switch (mode) {                                                                                      \
+        case 0: hipLaunchKernelGGL((k_dw_win<K, S, false, false>), grid, dim3(256), lds, g_stream, a); break; \
+        case 1: hipLaunchKernelGGL((k_dw_win<K, S, true, false>), grid, dim3(256), lds, g_stream, a); break;  \
+        case 2: hipLaunchKernelGGL((k_dw_win<K, S, false, true>), grid, dim3(256), lds, g_stream, a); break;  \
+        default: hipLaunchKernelGGL((k_dw_win<K, S, true, true>), grid, dim3(256), lds, g_stream, a); break;  \
+        }                                                                                                    \
+    } while (0)
+    if (d->kh == 3 && d->sh == 1) UQK_DWW(3, 1);
+    else if (d->kh == 3) UQK_DWW(3, 2);
+    else if (d->sh == 1) UQK_DWW(5, 1);
+    else UQK_DWW(5, 2);
+#undef UQK_DWW
+    UQK_LAUNCHED();
+    return 0;
+}
+
 // Tile geometry for k_dw_tile; returns the dynamic LDS bytes, 0 if unsuited.
 static size_t dw_tile_plan(const UQKSpatial *d, uint32_t batches, DwTileArgs *t)
 {
@@ -898,6 +1147,7 @@ static int launch_window(const UQKSpatial *d, const void *x, void *y, uint32_t b
 extern "C" int uqk_depthwise(const UQKSpatial *d, const void *x, void *y, uint32_t batches)
 {
     if (!batches) return 0;
+    if (d->dwwin) return launch_dw_win(d, x, y, batches) < 0 ? (int)hipErrorInvalidValue : 0;
     const int rc = launch_dw_tile(d, x, y, batches);
     if (rc >= 0) return rc;
     return launch_window(d, x, y, batches, false);

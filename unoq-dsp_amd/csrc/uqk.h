@@ -27,7 +27,8 @@ typedef struct {
     int32_t kh, kw, sh, sw, dh, dw, pt, pl;
     int32_t xz, yz, lo, hi;
     int32_t K, kpad, oc_pad, mode, nt, rb, is_max, vec, corr;
-    int32_t hi_shift;          /* conv, every shift in [-22, -1]: records fold bias and zero point into c1 */
+    int32_t hi_shift;          /* every shift in [-22, -1]: records fold bias and zero point into c1 */
+    int32_t dwwin;             /* depthwise on tap windows (k_dw_win); wdot holds [ky][wk][C] tap words */
     const void *w;
     const void *wdot;
     const void *epi;
@@ -39,6 +40,11 @@ typedef struct {
  * granularity, or LDS-staged input rows (16-byte slices, or 4-byte words
  * over channels padded to a multiple of four). */
 enum { UQK_PW = 0, UQK_G16 = 1, UQK_G4 = 2, UQK_G1 = 3, UQK_ROWS16 = 4, UQK_ROWS4 = 5 };
+
+/* Dynamic LDS bytes of the tap-window depthwise kernel for a layer, 0 when
+ * the layer's shape is outside it (needs C % 4 == 0, square 3x3 or 5x5,
+ * stride 1 or 2, no dilation). */
+size_t uqk_dw_win_lds(const UQKSpatial *d);
 
 /* Dynamic LDS bytes k_conv_rows needs for a layer at rb row blocks per wave. */
 size_t uqk_conv_rows_lds(const UQKSpatial *d, int rb);
