@@ -496,6 +496,22 @@ static ConvPlan conv_plan(const Op *o)
     c.nt = choose_nt(oc, (uint64_t)z->d[0] * z->d[1] * z->d[2]);
     c.oc_pad = (int)round_up((uint32_t)oc, (uint32_t)(16 * c.nt));
     int pointwise = q[0] == 1 && q[1] == 1 && q[2] == 1 && q[3] == 1 && !q[6] && !q[7] && !q[8] && !q[9];
+    UQKSpatial st;
+    memset(&st, 0, sizeof st);
+    st.iw = (int)G.ts[o->a].d[2]; st.ic = ic; st.kh = q[0]; st.sh = q[2]; st.dh = q[4];
+    if (ic <= 4 && q[0] * q[1] <= 16 && G.ts[o->a].rank == 4 && uqk_conv_stem_ok(&st)) {
+        /* Stem form: every tap one 4-byte word, one 64-byte K step; the
+         * channel slice spans the padded OC when that is at most 64. */
+        c.mode = UQK_STEM;
+        c.icp = 4;
+        c.K = q[0] * q[1] * 4;
+        c.kpad = 64;
+        int pad16 = (int)round_up((uint32_t)oc, 16);
+        c.nt = pad16 <= 16 ? 1 : pad16 <= 32 ? 2 : 4;
+        c.oc_pad = (int)round_up((uint32_t)oc, (uint32_t)(16 * c.nt));
+        c.table_bytes = 16;
+        return c;
+    }
     if (pointwise && ic % 16 == 0) {
         c.mode = UQK_PW;
         c.table_bytes = 16;
@@ -650,7 +666,7 @@ static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
                 int k = g * step, t = k / icp, c = k % icp, ky = t / q[1], kx = t % q[1];
                 kmap[g] = ((ky * q[4]) * cols + kx * q[5]) * icp + c;
             }
-        } else if (cp.mode != UQK_PW) {
+        } else if (cp.mode != UQK_PW && cp.mode != UQK_STEM) {
             int group = cp.mode == UQK_G16 ? 16 : cp.mode == UQK_G4 ? 4 : 1;
             for (int g = 0; g < K / group; g++) {
                 int k = g * group, t = k / ic, c = k % ic, ky = t / q[1], kx = t % q[1];

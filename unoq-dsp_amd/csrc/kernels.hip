@@ -111,6 +111,8 @@ struct ConvArgs {
     const uint8_t *lut;
     long M;
     int ih, iw, ic, icp, oh, ow, oc, kh, sh, sw, dh, pt, pl, xz, yz, lo, hi, K, kpad, ohw, corr, emode;
+    int kw, dw, taps;
+    int images, segs, row_groups, kw_magic, stem_rows;   // stem grid, tap decomposition, staged rows
     int tiles, cols, rows_max;
 };
 
@@ -503,6 +505,115 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
     conv_epilogue<RB, NT>(a, acc, stage, n0, lane, img0 + p0 + wave * R, img0 + pend, epi_s, lut_s);
 }
 
+// Stem convolution: at most four input channels and 16 taps (kh * kw), so
+// the receptive field of an output pixel, with every tap widened to a 4-byte
+// word, is a single 64-byte K step. A block is four waves on four consecutive
+// output rows of one image; each wave covers a 16*RB-pixel segment of its
+// row, so the image, the row and every kernel row's input row are
+// wave-uniform. The input rows the block touches are copied into LDS as they
+// are (rows of IW*IC bytes, 16-byte loads). Lane l supplies the A operand of
+// pixel l & 15 of a row block, K slice l >> 4 = taps 4s .. 4s + 3: each tap
+// is the four bytes at the pixel's input position (two aligned LDS words and
+// a byte shift); the bytes past the channel count land on zero weights, and
+// padding positions use the zero-point word.
+template <int RB, int NT>
+__global__ __launch_bounds__(256) void k_conv_stem(ConvArgs a)
+{
+    constexpr int R = RB * 16;
+    constexpr int STRIDE = NT * 16 + 16;
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    __shared__ __attribute__((aligned(16))) int8_t stage[4][R * STRIDE];
+    __shared__ __attribute__((aligned(4))) int8_t lut_s[256];
+    __shared__ int4 epi_s[2 * NT * 16];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    // blockIdx.x = (image * row_groups + row_group) * segments + segment
+    const int seg = blockIdx.x % a.segs;
+    const int rg = blockIdx.x / a.segs;
+    const int n = rg / a.row_groups, oy0 = (rg - n * a.row_groups) * 4, oy = oy0 + wave;
+    const bool row_ok = oy < a.oh;
+    const int ox0 = seg * R;
+    const int n0 = blockIdx.y * NT * 16;
+    const int xzw = (a.xz & 0xff) * 0x01010101;
+    const int rowbytes = a.iw * a.ic;                  // a multiple of 16 (host checked)
+    const int iy_base = oy0 * a.sh - a.pt;             // input row of staged row 0
+    const int8_t *xim = a.x + (long)n * a.ih * rowbytes;
+
+    const int8_t *wrow = a.w + (long)(n0 + lr) * a.kpad + lg * 16;
+    v4i B[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) B[nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad);
+
+    // Stage the rows (rows outside the image are never read).
+    const int chunks = rowbytes >> 4;
+    for (int r = 0; r < a.stem_rows; r++) {
+        const int iy = iy_base + r;
+        if ((unsigned)iy >= (unsigned)a.ih) continue;
+        const v4i *src = (const v4i *)(xim + (long)iy * rowbytes);
+        v4i *dst = (v4i *)(smem + r * rowbytes);
+        for (int c = threadIdx.x; c < chunks; c += 256) dst[c] = src[c];
+    }
+    stage_consts<NT>(a, n0, epi_s, lut_s);
+
+    // This lane's four taps: (ky, kx) of tap t = 4 * lg + j by a multiply-shift
+    // ((t * ceil(2^16 / kw)) >> 16 == t / kw for t, kw <= 16).
+    int ry[4], dx[4];
+    bool tap_ok[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int t = lg * 4 + j;
+        const int ky = (t * a.kw_magic) >> 16, kx = t - ky * a.kw;
+        const int iy = oy * a.sh - a.pt + ky * a.dh;
+        tap_ok[j] = t < a.taps && row_ok && (unsigned)iy < (unsigned)a.ih;
+        ry[j] = (iy - iy_base) * rowbytes;
+        dx[j] = kx * a.dw - a.pl;
+    }
+    __syncthreads();
+    const int *lw = (const int *)smem;
+    v4i A[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+        const int ox = ox0 + rb * 16 + lr;
+        int words[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int ix = ox * a.sw + dx[j];
+            int v = xzw;
+            if (tap_ok[j] && ox < a.ow && (unsigned)ix < (unsigned)a.iw) {
+                const int off = ry[j] + ix * a.ic;
+                const int lo = lw[off >> 2], hi = lw[(off >> 2) + 1];
+                v = (int)__builtin_amdgcn_alignbyte((unsigned)hi, (unsigned)lo, (unsigned)(off & 3));
+            }
+            words[j] = v;
+        }
+        A[rb] = (v4i){words[0], words[1], words[2], words[3]};
+    }
+    v4i acc[RB][NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+            acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[rb], B[nt], (v4i){0, 0, 0, 0}, 0, 0, 0);
+    // Rows of M for this wave: its output row, pixels ox0 .. min(ox0 + R, ow).
+    const long rbase = ((long)n * a.oh + oy) * a.ow + ox0;
+    const long rlimit = row_ok ? ((long)n * a.oh + oy) * a.ow + a.ow : rbase;
+    conv_epilogue<RB, NT>(a, acc, stage[wave], n0, lane, rbase, rlimit, epi_s, lut_s);
+}
+
+// Dynamic LDS of k_conv_stem (staged input rows plus one word of slack for
+// the second word of the last tap), 0 when the layer does not fit it: the
+// rows must be a multiple of 16 bytes and the staged rows at most 48 KiB.
+static size_t stem_lds(const UQKSpatial *d)
+{
+    const int rowbytes = d->iw * d->ic;
+    const int rows = 3 * d->sh + (d->kh - 1) * d->dh + 1;
+    const size_t bytes = (size_t)rows * rowbytes + 16;
+    return rowbytes % 16 == 0 && bytes <= 49152 ? bytes : 0;
+}
+
+extern "C" int uqk_conv_stem_ok(const UQKSpatial *d) { return stem_lds(d) > 0; }
+
 template <int RB, int NT>
 static void launch_conv_mode(int mode, const ConvArgs &a, dim3 grid, size_t lds)
 {
@@ -575,8 +686,38 @@ extern "C" int uqk_conv(const UQKSpatial *d, const void *x, void *y, uint32_t ba
     a.K = d->K; a.kpad = d->kpad; a.ohw = d->oh * d->ow; a.corr = d->corr;
     a.emode = (d->hi_shift ? 1 : 0) | (d->corr ? 2 : 0);
     a.cols = (d->ow - 1) * d->sw + (d->kw - 1) * d->dw + 1;
+    a.kw = d->kw; a.dw = d->dw; a.taps = d->kh * d->kw;
     if (a.M <= 0) return 0;
     const int nchunks = d->oc_pad / (16 * d->nt);
+    if (d->mode == UQK_STEM) {
+        // One row segment per wave, four rows per block; the channel
+        // slice covers up to 64 channels (NT = oc_pad / 16 when that is 1, 2
+        // or 4).
+        const int nt = d->oc_pad == 16 ? 1 : d->oc_pad == 32 ? 2 : 4;
+        a.images = (int)batches;
+        // 128-pixel segments (eight row blocks per wave) on wide rows: more
+        // loads in flight per wave.
+        const int rbk = d->ow > 64 ? 8 : 4;
+        a.segs = (d->ow + 16 * rbk - 1) / (16 * rbk);
+        a.row_groups = (d->oh + 3) / 4;
+        a.kw_magic = (65536 + d->kw - 1) / d->kw;
+        a.stem_rows = 3 * d->sh + (d->kh - 1) * d->dh + 1;
+        const size_t lds = stem_lds(d);
+        const unsigned long long blocks = (unsigned long long)batches * a.row_groups * a.segs;
+        if (!lds || blocks > 0x7fffffffULL) return (int)hipErrorInvalidValue;
+        dim3 grid((unsigned)blocks, (unsigned)(d->oc_pad / (16 * nt)));
+#define UQK_STEM_NT(RBK)                                                                                  \
+    do {                                                                                                  \
+        if (nt == 1) hipLaunchKernelGGL((k_conv_stem<RBK, 1>), grid, dim3(256), lds, g_stream, a);       \
+        else if (nt == 2) hipLaunchKernelGGL((k_conv_stem<RBK, 2>), grid, dim3(256), lds, g_stream, a);  \
+        else hipLaunchKernelGGL((k_conv_stem<RBK, 4>), grid, dim3(256), lds, g_stream, a);               \
+    } while (0)
+        if (rbk == 8) UQK_STEM_NT(8);
+        else UQK_STEM_NT(4);
+#undef UQK_STEM_NT
+        UQK_LAUNCHED();
+        return 0;
+    }
     if (d->mode == UQK_ROWS16 || d->mode == UQK_ROWS4) {
         // Larger tiles stage fewer redundant input rows per output row.
         const int rb = d->mode == UQK_ROWS4 && d->nt <= 4 && uqk_conv_rows_lds(d, 4) <= 65536 ? 4 : 2, bm = 4 * 16 * rb;
@@ -1220,9 +1361,40 @@ __global__ __launch_bounds__(256) void k_mean(const int8_t *x, int8_t *y, uint32
     y[idx] = (int8_t)min(max(uq_scale(sum - (int)pixels * xz, m, s) + yz, -128), 127);
 }
 
+// Four channels per thread (one dword per pixel) when C % 4 == 0; the pixel
+// loop is unrolled so that several loads are in flight.
+__global__ __launch_bounds__(256) void k_mean4(const int8_t *x, int8_t *y, uint32_t batches, uint32_t pixels,
+                                                uint32_t channels, int xz, int yz, int m, int s)
+{
+    const uint32_t groups = channels >> 2;
+    const uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (uint64_t)batches * groups) return;
+    const uint32_t n = (uint32_t)(idx / groups), g = (uint32_t)(idx - (uint64_t)n * groups);
+    const int8_t *p = x + (uint64_t)n * pixels * channels + 4 * g;
+    int sum[4] = {0, 0, 0, 0};
+#pragma unroll 8
+    for (uint32_t q = 0; q < pixels; q++) {
+        const int w = *(const int *)(p + (uint64_t)q * channels);
+#pragma unroll
+        for (int j = 0; j < 4; j++) sum[j] += sbyte(w, j);
+    }
+    int v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = min(max(uq_scale(sum[j] - (int)pixels * xz, m, s) + yz, -128), 127);
+    *(int *)(y + (uint64_t)n * channels + 4 * g) = pack4(v[0], v[1], v[2], v[3]);
+}
+
 extern "C" int uqk_mean(const void *x, void *y, uint32_t batches, uint32_t pixels, uint32_t channels,
                         int32_t xz, int32_t yz, int32_t m, int32_t shift)
 {
+    if (channels % 4 == 0) {
+        const uint64_t total = (uint64_t)batches * (channels / 4);
+        if (!total) return 0;
+        hipLaunchKernelGGL(k_mean4, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g_stream,
+                           (const int8_t *)x, (int8_t *)y, batches, pixels, channels, xz, yz, m, shift);
+        UQK_LAUNCHED();
+        return 0;
+    }
     const uint64_t total = (uint64_t)batches * channels;
     if (!total) return 0;
     hipLaunchKernelGGL(k_mean, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g_stream,

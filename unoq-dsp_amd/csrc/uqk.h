@@ -37,14 +37,20 @@ typedef struct {
 } UQKSpatial;
 
 /* Conv A-operand sources: pointwise rows, per-lane gathers with 16/4/1-byte
- * granularity, or LDS-staged input rows (16-byte slices, or 4-byte words
- * over channels padded to a multiple of four). */
-enum { UQK_PW = 0, UQK_G16 = 1, UQK_G4 = 2, UQK_G1 = 3, UQK_ROWS16 = 4, UQK_ROWS4 = 5 };
+ * granularity, LDS-staged input rows (16-byte slices, or 4-byte words over
+ * channels padded to a multiple of four), or the stem form (at most four
+ * input channels and 16 taps: every tap is one 4-byte word read straight
+ * from the input and the receptive field is one 64-byte K step). */
+enum { UQK_PW = 0, UQK_G16 = 1, UQK_G4 = 2, UQK_G1 = 3, UQK_ROWS16 = 4, UQK_ROWS4 = 5, UQK_STEM = 6 };
 
 /* Dynamic LDS bytes of the tap-window depthwise kernel for a layer, 0 when
  * the layer's shape is outside it (needs C % 4 == 0, square 3x3 or 5x5,
  * stride 1 or 2, no dilation). */
 size_t uqk_dw_win_lds(const UQKSpatial *d);
+
+/* Whether a conv layer fits the stem kernel's row staging (input rows a
+ * multiple of 16 bytes, staged rows within 48 KiB). */
+int uqk_conv_stem_ok(const UQKSpatial *d);
 
 /* Dynamic LDS bytes k_conv_rows needs for a layer at rb row blocks per wave. */
 size_t uqk_conv_rows_lds(const UQKSpatial *d, int rb);
