@@ -176,6 +176,27 @@ static void bmm_image(const Ten *a, const Ten *b, const Ten *z, const int8_t *x,
     (void)b;
 }
 
+/* Code 17, qnn.c:1082-1087: per row of q[16] values, e_j = table[max - x_j]
+ * (table = q[20..275], Q24 with table[0] = 2^24), y_j = round(256 e_j / S)
+ * with S = sum e_j (64-bit, halves rounded up), minus 128, clamped to
+ * [q14, q15]. */
+static void softmax_table_image(const int8_t *x, int8_t *y, uint32_t bytes, const int32_t *q)
+{
+    uint32_t width = (uint32_t)q[16];
+    const int32_t *table = q + HEAD;
+    for (uint32_t base = 0; base < bytes; base += width) {
+        int mx = -128;
+        for (uint32_t j = 0; j < width; j++) if (x[base + j] > mx) mx = x[base + j];
+        uint64_t sum = 0;
+        for (uint32_t j = 0; j < width; j++) sum += (uint32_t)table[mx - x[base + j]];
+        for (uint32_t j = 0; j < width; j++) {
+            uint64_t v = (uint64_t)(uint32_t)table[mx - x[base + j]] * 256;
+            int32_t r = (int32_t)((v + sum / 2) / sum) - 128;
+            y[base + j] = clampi(r, q[14], q[15]);
+        }
+    }
+}
+
 /* Rounding doubling high multiply, qnn.c:61-70 with shift 0. */
 static int32_t high_mul(int32_t a, int32_t b) { return uqo_scale(a, b, 0); }
 
@@ -268,6 +289,7 @@ int uqo_run(const void *plan, uint32_t len, const void *input, uint32_t images,
             const int8_t *ap = (const int8_t *)AT(o->a, j), *bp = (const int8_t *)AT(o->b, j);
             int8_t *zp = (int8_t *)AT(o->out, j);
             switch (o->code) {
+            case 17: softmax_table_image(ap, zp, a->bytes, (const int32_t *)CONST(o->p[0])); break;
             case 14: case 15: case 16: {
                 const int32_t *q = (const int32_t *)CONST(o->p[0]);
                 const uint8_t *lut = (o->code != 16 && o->p[1]) ? CONST(o->p[1] - 1) : NULL;

@@ -138,7 +138,8 @@ def transpose_op(p, rng, x):
 
 def attention_op(p, rng, x):
     """Self-attention on rank-3 views, as the detector's attention block:
-    S = bmm(Q, K^T), P = softmax(S), O = bmm(V, P^T) or bmm(P, V)."""
+    S = bmm(Q, K^T), P = softmax(S) (exact code 28 or table code 17),
+    O = bmm(P, V)."""
     n, h, w, c = p.shape(x)
     q = p.copy(x, (n * h, w, c))
     kq = p.lut(q, _random_lut(p, rng))
@@ -147,7 +148,7 @@ def attention_op(p, rng, x):
     ta = _pick(rng, [0, 0, 1])
     a = p.transpose(q, (0, 2, 1)) if ta else q
     scores = p.bmm(a, k_op, trans_a=bool(ta), trans_b=bool(kt_stored))   # [B][w][w]
-    probs = p.softmax(scores)
+    probs = p.softmax(scores) if _pick(rng, [0, 0, 1]) == 0 else p.softmax_table(scores)
     v = p.lut(q, _random_lut(p, rng))                                  # [B][w][c]
     out = p.bmm(probs, v)                                              # [B][w][c]
     return p.copy(out, (n, h, w, c))

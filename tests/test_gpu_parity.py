@@ -11,7 +11,8 @@ import pytest
 import uq_plan as P
 import uq_workloads as W
 from plan_fuzz import ATTENTION_OPS, CONSTANT_OPS, random_plan
-from test_oracle_vs_reference import BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, transpose_plan
+from test_oracle_vs_reference import (BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, softmax_table_plan,
+                                      transpose_plan)
 from refs import oracle_run
 from uq_native import DeviceBuffer, Graph, NativeError, open_library
 
@@ -104,6 +105,16 @@ def test_softmax(lib, width, beta_scale):
     x = P.random_input(plan, images, width)
     x[:3 * width] = np.repeat(np.array([-128, 0, 127], np.int8), width)   # all-tie rows
     _assert_same(Graph(plan, lib).run_batch(x, images), _oracle(plan, x, images), f"softmax w={width}")
+
+
+@pytest.mark.parametrize("width", [1, 17, 100, 2048])
+@pytest.mark.parametrize("beta_scale", [0.001, 16.0])
+def test_softmax_table(lib, width, beta_scale):
+    plan = softmax_table_plan(width, beta_scale)
+    images = 5
+    x = P.random_input(plan, images, width)
+    x[:3 * width] = np.repeat(np.array([-128, 0, 127], np.int8), width)
+    _assert_same(Graph(plan, lib).run_batch(x, images), _oracle(plan, x, images), f"softmax17 w={width}")
 
 
 @pytest.mark.parametrize("shape,perm", TRANSPOSES)

@@ -5,6 +5,7 @@ constant-channel elimination, fixed depthwise kernels) and the plain build.
 
 Pins: conv_image (code 14), window_image (codes 15 and 16), add_image,
 mean_image, mul_image (25), bmm_image (27), softmax_image (28),
+softmax_table_image (17),
 transpose_image (10) and the byte ops 5/19/20/21/22/23/26 of uqo_run, plus
 the whole of both shipped models (MobileNetV4-small, YOLO26n-320 with its
 attention block) where the reference tree is present. The reference's
@@ -133,6 +134,23 @@ def test_softmax_widths_and_scales(width, beta_scale):
     _check_plan(plan, 2, width)
     # Rows of one repeated value (ties everywhere; the widest rows reach the
     # exponent >= 32 branch).
+    xin = np.repeat(np.array([-128, 0, 127], np.int8), width)
+    rel = ref_release()
+    assert rel.load(plan) == 0
+    np.testing.assert_array_equal(oracle_run(plan, xin, 1, P.output_bytes(plan)), rel.run_images(xin, 1))
+
+
+def softmax_table_plan(width, beta_scale, rows=3, zp=-17):
+    p = P.Plan(width + 1)
+    x = p.input((rows, width), zp=zp)
+    return p.build(p.softmax_table(x, beta_scale=beta_scale))
+
+
+@pytest.mark.parametrize("width", [1, 2, 17, 100, 256, 2048])
+@pytest.mark.parametrize("beta_scale", [0.001, 0.17, 16.0])
+def test_softmax_table_widths_and_scales(width, beta_scale):
+    plan = softmax_table_plan(width, beta_scale)
+    _check_plan(plan, 2, width)
     xin = np.repeat(np.array([-128, 0, 127], np.int8), width)
     rel = ref_release()
     assert rel.load(plan) == 0

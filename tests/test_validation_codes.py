@@ -21,7 +21,7 @@ from plan_fuzz import random_plan
 from refs import ref_plain, ref_release
 from uq_native import open_library
 
-SUPPORTED = {5, 10, 14, 15, 16, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28}
+SUPPORTED = {5, 10, 14, 15, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28}
 
 
 @pytest.fixture(scope="module")

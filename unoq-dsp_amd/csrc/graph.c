@@ -439,8 +439,8 @@ static int validate(const uint8_t *p, uint32_t len)
 static int supported(uint32_t code)
 {
     switch (code) {
-    case 5: case 10: case 14: case 15: case 16: case 18: case 19: case 20: case 21: case 22: case 23: case 24:
-    case 25: case 26: case 27: case 28: return 1;
+    case 5: case 10: case 14: case 15: case 16: case 17: case 18: case 19: case 20: case 21: case 22: case 23:
+    case 24: case 25: case 26: case 27: case 28: return 1;
     default: return 0;
     }
 }
@@ -836,6 +836,13 @@ static int enqueue_ops(uint32_t images)
             break;
         case 22: rc = uqk_lut(ap, zp, (uint64_t)images * a->bytes, bp, a->type == 3 ? 128u : 0u); break;
         case 10: rc = uqk_permute(ap, zp, images, a->rank, a->d, o->p, width(a->type)); break;
+        case 17: {
+            const int32_t *q = (const int32_t *)(A + G.ts[o->p[0]].offset);
+            const uint32_t w = (uint32_t)q[16];
+            rc = uqk_softmax_table(ap, zp, (uint64_t)images * (z->bytes / w), w,
+                                   G.dev_arena + G.ts[o->p[0]].offset + UQ_HEAD * 4, q[14], q[15]);
+            break;
+        }
         case 25: rc = uqk_mul(ap, bp, zp, (uint64_t)images * z->bytes, (const int32_t *)(A + G.ts[o->p[0]].offset)); break;
         case 27: {
             const int32_t *q = (const int32_t *)(A + G.ts[o->p[0]].offset);

@@ -1740,6 +1740,49 @@ __global__ __launch_bounds__(256) void k_softmax(const int8_t *x, int8_t *y, uin
     }
 }
 
+// Table softmax (code 17, qnn.c:1082-1087): one wave per row; the 64-bit sum
+// of Q24 table exponentials is a wave reduction, each element one exact
+// 64-bit rounded division.
+__global__ __launch_bounds__(256) void k_softmax_table(const int8_t *x, int8_t *y, uint64_t rows, uint32_t width,
+                                                        const int *table, int lo, int hi)
+{
+    __shared__ int lut[256];
+    lut[threadIdx.x] = table[threadIdx.x];
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63;
+    const uint64_t row = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int8_t *src = x + row * width;
+    int mx = -128;
+    for (uint32_t j = lane; j < width; j += 64) mx = max(mx, (int)src[j]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = max(mx, __shfl_xor(mx, off, 64));
+    unsigned long long sum = 0;
+    for (uint32_t j = lane; j < width; j += 64) sum += (unsigned)lut[mx - (int)src[j]];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned lo32 = __shfl_xor((unsigned)sum, off, 64), hi32 = __shfl_xor((unsigned)(sum >> 32), off, 64);
+        sum += ((unsigned long long)hi32 << 32) | lo32;
+    }
+    const unsigned long long half = sum / 2;
+    int8_t *dst = y + row * width;
+    for (uint32_t j = lane; j < width; j += 64) {
+        const unsigned long long v = (unsigned long long)(unsigned)lut[mx - (int)src[j]] * 256ull;
+        const int r = (int)((v + half) / sum) - 128;
+        dst[j] = (int8_t)min(max(r, lo), hi);
+    }
+}
+
+extern "C" int uqk_softmax_table(const void *x, void *y, uint64_t rows, uint32_t width, const void *table, int32_t lo,
+                                 int32_t hi)
+{
+    if (!rows) return 0;
+    hipLaunchKernelGGL(k_softmax_table, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, g_stream, (const int8_t *)x,
+                       (int8_t *)y, rows, width, (const int *)table, lo, hi);
+    UQK_LAUNCHED();
+    return 0;
+}
+
 extern "C" int uqk_softmax(const void *x, void *y, uint64_t rows, uint32_t width, const void *table)
 {
     if (!rows) return 0;

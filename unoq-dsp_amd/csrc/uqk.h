@@ -93,6 +93,9 @@ int uqk_bmm(const void *a, const void *b, void *z, uint32_t images, uint32_t bat
 /* Exact softmax (code 28) over rows of `width` bytes; table = 256 Q0.31 exponentials. */
 int uqk_softmax(const void *x, void *y, uint64_t rows, uint32_t width, const void *table);
 
+/* Table softmax (code 17) over rows of `width` bytes; table = 256 Q24 values. */
+int uqk_softmax_table(const void *x, void *y, uint64_t rows, uint32_t width, const void *table, int32_t lo, int32_t hi);
+
 /* Timing: a pool of HIP events recorded on the library stream. */
 int uqk_events(uint32_t count);
 int uqk_record(uint32_t index);

@@ -456,6 +456,24 @@ class Plan:
         self._op(28, x, bt, z)
         return z
 
+    def softmax_table(self, x, beta_scale=None):
+        """Code 17: table softmax (qnn.c:1082-1087), q = 20 header words
+        (q[13] = q[14] = -128, q[15] = 127, q[16] = width) then 256 Q24
+        exponentials exp(-d * beta_scale) * 2^24."""
+        rng = self.rng()
+        if beta_scale is None:
+            beta_scale = float(0.01 + 0.3 * rng.uniform01(1)[0])
+        d = np.arange(256, dtype=np.float64)
+        table = np.round(np.exp(-d * beta_scale) * 2.0 ** 24).astype(np.int64)
+        table[0] = 1 << 24
+        q = [0] * 20
+        q[12], q[13], q[14], q[15], q[16] = self.zp[x], -128, -128, 127, self.shape(x)[-1]
+        qt = self.tensor((276,), TYPE_I32, np.concatenate((q, table)))
+        z = self.tensor(self.shape(x))
+        self.zp[z] = -128
+        self._op(17, x, x, z, (qt, 0, 0, 0))
+        return z
+
     # -- serialisation -----------------------------------------------------
     def build(self, output, version=2):
         hdr = struct.pack("<8I", MAGIC, version, len(self.tensors), len(self.ops), len(self.arena),
