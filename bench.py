@@ -132,6 +132,46 @@ def committed_traffic(workload, op):
     return None, None
 
 
+def host_transfer(lib, steps):
+    """MobileNetV4-S from pinned host buffers, PCIe included: 1024 images as
+    one blocking batch call against the pipelined call in 256-image chunks
+    (host-to-device copies of one chunk under the compute of the previous),
+    and batch-1 latency through the session ABI in its two modes."""
+    plan, _ = W.WORKLOADS["mnv4"]()
+    images = 1024
+    g = Graph(plan, lib)
+    ib, ob = g.input_bytes, g.output_bytes
+    x = P.random_input(plan, images, 5)
+    hin, hout = lib.ug_host_alloc(x.nbytes), lib.ug_host_alloc(images * ob)
+    C.memmove(hin, x.ctypes.data, x.nbytes)
+    res = {"images": images, "input_mb": round(x.nbytes / 1e6, 2)}
+
+    def timed(fn):
+        fn()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        return (time.perf_counter() - t0) / steps
+
+    def blocking():
+        assert lib.ug_run_batch(hin, x.nbytes, hout, images * ob, images) == 0
+
+    def pipelined():
+        assert lib.ug_run_batch_pipelined(hin, x.nbytes, hout, images * ob, images, 256) == 0
+
+    for key, fn in (("blocking", blocking), ("pipelined", pipelined)):
+        sec = timed(fn)
+        res[key] = {"ms": round(sec * 1e3, 3), "images_per_s": round(images / sec, 1)}
+    lib.ug_host_free(hin)
+    lib.ug_host_free(hout)
+    from uq_native import Session
+    for mode in ("rpc", "mailbox"):
+        with Session(plan, mode, lib) as s:
+            one = x[:ib]
+            res[f"latency_b1_{mode}_ms"] = round(timed(lambda: s.run(one)) * 1e3, 4)
+    return res
+
+
 def secondary(lib, steps):
     out = {}
     plan, images = W.WORKLOADS["yolo"]()
@@ -146,6 +186,7 @@ def secondary(lib, steps):
         ops = sum(c["ops"] for c in P.op_costs(plan, images))
         out[name] = {"images": images, "ms": round(sec / steps * 1e3, 4), "tops": round(ops / (sec / steps) / 1e12, 2),
                      "kernel_tops": round(ops / (per_op.sum() * 1e-9) / 1e12, 2)}
+    out["host_transfer"] = host_transfer(lib, max(steps // 2, 3))
     for name in ("dw3s1", "dw3s2", "dw5s1", "dw5s2"):
         plan, images = W.WORKLOADS[name]()
         g = Graph(plan, lib)

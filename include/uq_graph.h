@@ -91,6 +91,19 @@ int ug_device_download(void *dst, const void *d_src, uint64_t bytes);
 /* Number of ops of the loaded plan, 0 when not loaded. */
 uint32_t ug_op_count(void);
 
+/* Host-buffer batch with transfers overlapped with compute: the batch runs in
+ * chunks of `chunk` images (0: chunks of max(256, images/8) images from 512
+ * images on, unchunked below); chunk k's host-to-device copy, chunk k-1's
+ * kernels and chunk k-2's copy back proceed on three streams at once.
+ * Same sizes and codes as ug_run_batch. Afterwards snapshots hold the last
+ * chunk. Host buffers from ug_host_alloc transfer by DMA at full rate;
+ * ordinary pageable memory also works, with less overlap. */
+int ug_run_batch_pipelined(const void *input, uint64_t ni, void *output, uint64_t no, uint32_t images, uint32_t chunk);
+
+/* Pinned host memory for the host-buffer entry points (NULL without a GPU). */
+void *ug_host_alloc(uint64_t bytes);
+int ug_host_free(void *p);
+
 /* ---- Part 3: .uqmodel bundles (src/unoq_dsp/bundle.py:18-19, 84-141) ---- */
 
 /* Check a bundle image (header, lengths, SHA-256 of manifest || plan, plan
@@ -107,6 +120,37 @@ int ug_load_bundle(const void *file, uint64_t len);
 
 /* SHA-256 of a byte string (FIPS 180-4), the bundle checksum. */
 void uq_sha256(const void *data, uint64_t len, uint8_t out[32]);
+
+/* ---- Part 4: the reference's host session ABI (runtime/bridge.c) -------- */
+/* The entry points the reference's Python HardwareSession binds
+ * (src/unoq_dsp/transport.py:35-43), with the same argument checks and codes.
+ * One session at a time over the library's single model. */
+
+/* bridge.c:99-125. Load the plan and open a session; NULL on failure with
+ * *error = 1 (bad arguments: null plan, more than 17 MiB, pipeline not 0/1),
+ * 1001 (a session is open), 1002 (allocation), the ug_load code, or 0 when
+ * the plan's input or output exceeds 4 MiB. pipeline 0 is the blocking call
+ * per image ("rpc"); 1 ("mailbox") replays one captured graph of the whole
+ * plan through pinned staging buffers, for the lowest per-call latency. */
+void *ug_open_mode(const void *plan, uint32_t bytes, int pipeline, int *error);
+
+/* bridge.c:126: ug_open_mode(plan, bytes, 0, error). */
+void *ug_open(const void *plan, uint32_t bytes, int *error);
+
+/* bridge.c:148-185. One image: 1003 on a null session/buffer or sizes other
+ * than the model's; otherwise ug_run's codes. */
+int ug_infer(void *session, const void *input, uint32_t ni, void *output, uint32_t no);
+
+/* bridge.c:70-80. Ends the session (the model stays loaded); null is a no-op. */
+void ug_close(void *session);
+
+/* bridge.c:127-130. ug_snapshot through the session; 1003 in pipeline mode or
+ * for a null session/buffer or bytes outside 1 .. 4 MiB. */
+int ug_snapshot_tensor(void *session, uint32_t index, void *out, uint32_t bytes);
+
+/* bridge.c:134-147. ug_profile through the session; 1003 for a null session or
+ * buffer, a command above 2, or bytes other than 130*8 or 514*8. */
+int ug_profile_control(void *session, uint32_t command, void *out, uint32_t bytes);
 
 #ifdef __cplusplus
 }

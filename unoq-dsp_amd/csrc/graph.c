@@ -19,6 +19,7 @@
 #define UG_MAGIC 0x55474e31u
 #define UG_MAX_T 1024u
 #define UG_MAX_OP 512u
+#define UG_MAX_PLAN (17u * 1024u * 1024u)
 #define UG_ARENA (16u * 1024u * 1024u)
 #define UG_MAX_WORK 2000000000ULL
 #define UQ_HEAD 20
@@ -44,6 +45,9 @@ static struct {
     uint32_t capacity, last_images;
     UQKSpatial sp[UG_MAX_OP];
     uint64_t ticks[UG_MAX_OP + 2];
+    uint64_t generation;         /* bumped whenever device buffers move (graphs must be re-captured) */
+    uint8_t *pipe_in[2], *pipe_out[2]; /* device chunk buffers of the pipelined batch */
+    uint64_t pipe_in_bytes, pipe_out_bytes;
 } G;
 
 static uint32_t width(uint32_t t) { return t == 1 || t == 4 ? 4 : t == 2 || t == 3 ? 1 : 0; }
@@ -454,8 +458,15 @@ static void release_device(void)
     uqk_free(G.dev_arena);
     uqk_free(G.dev_prep);
     G.dev_arena = G.dev_prep = NULL;
+    for (int k = 0; k < 2; k++) {
+        uqk_free(G.pipe_in[k]);
+        uqk_free(G.pipe_out[k]);
+        G.pipe_in[k] = G.pipe_out[k] = NULL;
+    }
+    G.pipe_in_bytes = G.pipe_out_bytes = 0;
     G.capacity = 0;
     G.last_images = 0;
+    G.generation++;
 }
 
 static uint32_t round_up(uint32_t v, uint32_t m) { return (v + m - 1) / m * m; }
@@ -789,6 +800,7 @@ static int ensure_capacity(uint32_t images)
         G.act[t] = NULL;
     }
     G.capacity = 0;
+    G.generation++;
     for (uint32_t t = 0; t < G.h.nt; t++) {
         if (G.ts[t].flags && !G.bcast[t]) continue;
         G.act[t] = uqk_malloc((size_t)images * G.ts[t].bytes);
@@ -997,6 +1009,210 @@ int ug_run_device(const void *d_input, void *d_output, uint32_t images)
     int rc = ug_enqueue_device(d_input, d_output, images);
     if (rc) return rc;
     return ug_synchronize();
+}
+
+/* Chunked host-buffer batch with transfers overlapped with compute: chunk k's
+ * host-to-device copy runs on the copy-in stream while chunk k-1 computes and
+ * chunk k-2's results copy back on the copy-out stream. Two device buffers
+ * per direction; events order reuse (a slot's input is overwritten only after
+ * the chunk that read it finished, its output only after its copy-back). */
+int ug_run_batch_pipelined(const void *input, uint64_t ni, void *output, uint64_t no, uint32_t images, uint32_t chunk)
+{
+    if (!G.ready || !input || !output || !images || ni != (uint64_t)images * ug_input_bytes() ||
+        no != (uint64_t)images * ug_output_bytes())
+        return 22;
+    const Tensor *t = G.ts + G.h.output;
+    /* Auto: chunks of at least 256 images (smaller launches underfill the
+     * chip, which costs more than the overlap gains), pipelined from 512. */
+    if (!chunk) chunk = images >= 512 ? ((images + 7) / 8 > 256 ? (images + 7) / 8 : 256) : images;
+    if (chunk > images) chunk = images;
+    /* Profiling records per-op events on the compute stream, and a constant
+     * output needs no device work: both take the single-stream path. */
+    if (G.profile_enabled || t->flags || chunk == images) return ug_run_batch(input, ni, output, no, images);
+    const uint64_t ib = ug_input_bytes(), ob = ug_output_bytes();
+    if (ensure_capacity(chunk)) return fail(24);
+    if (G.pipe_in_bytes < (uint64_t)chunk * ib || G.pipe_out_bytes < (uint64_t)chunk * ob) {
+        if (uqk_sync_all()) return fail(24);
+        for (int k = 0; k < 2; k++) {
+            uqk_free(G.pipe_in[k]);
+            uqk_free(G.pipe_out[k]);
+            G.pipe_in[k] = uqk_malloc((size_t)chunk * ib);
+            G.pipe_out[k] = uqk_malloc((size_t)chunk * ob);
+            if (!G.pipe_in[k] || !G.pipe_out[k]) return fail(24);
+        }
+        G.pipe_in_bytes = (uint64_t)chunk * ib;
+        G.pipe_out_bytes = (uint64_t)chunk * ob;
+        G.generation++;
+    }
+    /* events: 0/1 input slot loaded, 2/3 slot computed, 4/5 output slot copied back */
+    const uint32_t chunks = (images + chunk - 1) / chunk;
+    uint32_t last = chunk;
+    for (uint32_t k = 0; k < chunks; k++) {
+        const int slot = (int)(k & 1);
+        const uint32_t nk = (k + 1) * chunk <= images ? chunk : images - k * chunk;
+        const uint8_t *src = (const uint8_t *)input + (size_t)k * chunk * ib;
+        uint8_t *dst = (uint8_t *)output + (size_t)k * chunk * ob;
+        if (k >= 2 && uqk_pipe_wait(1, 2 + slot)) return fail(24);
+        if (uqk_copy_on(1, G.pipe_in[slot], src, (size_t)nk * ib, 1) || uqk_pipe_record(slot, 1)) return fail(24);
+        if (uqk_pipe_wait(0, slot)) return fail(24);
+        if (k >= 2 && uqk_pipe_wait(0, 4 + slot)) return fail(24);
+        bind_pointers(G.pipe_in[slot], G.pipe_out[slot]);
+        if (enqueue_ops(nk) || deliver_output_device(G.pipe_out[slot], nk)) return fail(24);
+        if (uqk_pipe_record(2 + slot, 0)) return fail(24);
+        if (uqk_pipe_wait(2, 2 + slot)) return fail(24);
+        if (uqk_copy_on(2, dst, G.pipe_out[slot], (size_t)nk * ob, 0) || uqk_pipe_record(4 + slot, 2)) return fail(24);
+        last = nk;
+    }
+    if (uqk_sync_all()) return fail(24);
+    /* Snapshots see the last chunk's tensors. */
+    G.last_images = last;
+    return 0;
+}
+
+void *ug_host_alloc(uint64_t bytes)
+{
+    if (uqk_init()) return NULL;
+    return uqk_host_alloc((size_t)bytes);
+}
+
+int ug_host_free(void *p)
+{
+    uqk_host_free(p);
+    return 0;
+}
+
+/* ---- Bridge ABI: the reference's host session (runtime/bridge.c:99-185) ---
+ * One session at a time over the library's single model. Mode 0 ("rpc") runs
+ * each ug_infer through ug_run. Mode 1 ("mailbox", the persistent-worker
+ * pipeline of the DSP host) keeps the per-call path short instead: pinned
+ * staging buffers and one captured graph of the whole plan, replayed per
+ * call. */
+typedef struct {
+    int pipeline;
+    uint32_t ni, no;
+    uint8_t *h_in, *h_out;      /* pinned staging (mailbox mode) */
+    uint8_t *d_in, *d_out;      /* device buffers of one image (mailbox mode) */
+    void *graph;
+    uint64_t generation;
+} Session;
+
+static Session *g_session;
+
+static void session_release(Session *s)
+{
+    uqk_graph_destroy(s->graph);
+    uqk_host_free(s->h_in);
+    uqk_host_free(s->h_out);
+    uqk_free(s->d_in);
+    uqk_free(s->d_out);
+    free(s);
+}
+
+void ug_close(void *ptr)
+{
+    Session *s = ptr;
+    if (!s || s != g_session) return;
+    (void)uqk_sync();
+    session_release(s);
+    g_session = NULL;
+}
+
+void *ug_open_mode(const void *plan, uint32_t bytes, int pipeline, int *error)
+{
+    if (!error) return NULL;
+    *error = 1;
+    if (!plan || bytes > UG_MAX_PLAN || pipeline < 0 || pipeline > 1) return NULL;
+    if (g_session) {
+        *error = 1001;
+        return NULL;
+    }
+    int rc = ug_load(plan, bytes);
+    if (rc) {
+        *error = rc;
+        return NULL;
+    }
+    uint32_t ni = ug_input_bytes(), no = ug_output_bytes();
+    if (!ni || !no || ni > 4u * 1024 * 1024 || no > 4u * 1024 * 1024) {
+        /* bridge.c:117 reports the loader's (zero) code for oversized I/O. */
+        *error = 0;
+        return NULL;
+    }
+    Session *s = calloc(1, sizeof *s);
+    if (!s) {
+        *error = 1002;
+        return NULL;
+    }
+    s->pipeline = pipeline;
+    s->ni = ni;
+    s->no = no;
+    if (pipeline) {
+        s->h_in = uqk_host_alloc(ni);
+        s->h_out = uqk_host_alloc(no);
+        s->d_in = uqk_malloc(ni);
+        s->d_out = uqk_malloc(no);
+        if (!s->h_in || !s->h_out || !s->d_in || !s->d_out) {
+            session_release(s);
+            *error = 1002;
+            return NULL;
+        }
+    }
+    g_session = s;
+    *error = 0;
+    return s;
+}
+
+void *ug_open(const void *plan, uint32_t bytes, int *error) { return ug_open_mode(plan, bytes, 0, error); }
+
+/* Capture the whole plan for one image on the session's device buffers. */
+static int session_capture(Session *s)
+{
+    uqk_graph_destroy(s->graph);
+    s->graph = NULL;
+    if (ensure_capacity(1)) return 24;
+    bind_pointers(s->d_in, s->d_out);
+    if (uqk_capture_begin()) return 24;
+    int rc = enqueue_ops(1);
+    if (!rc) rc = deliver_output_device(s->d_out, 1);
+    void *exec = NULL;
+    int end = uqk_capture_end(&exec);
+    if (rc || end) {
+        uqk_graph_destroy(exec);
+        return 24;
+    }
+    s->graph = exec;
+    s->generation = G.generation;
+    return 0;
+}
+
+int ug_infer(void *ptr, const void *in, uint32_t ni, void *out, uint32_t no)
+{
+    Session *s = ptr;
+    if (!s || s != g_session || !in || !out || ni != s->ni || no != s->no) return 1003;
+    if (!s->pipeline || G.profile_enabled || G.ts[G.h.output].flags) return ug_run(in, ni, out, no);
+    if (!G.ready || ug_input_bytes() != ni || ug_output_bytes() != no) return 22;
+    if ((!s->graph || s->generation != G.generation) && session_capture(s)) return fail(24);
+    memcpy(s->h_in, in, ni);
+    if (uqk_h2d(s->d_in, s->h_in, ni) || uqk_graph_launch(s->graph) || uqk_d2h(s->h_out, s->d_out, no) || uqk_sync())
+        return fail(24);
+    memcpy(out, s->h_out, no);
+    /* The captured run bound the tensors to this session's buffers. */
+    bind_pointers(s->d_in, s->d_out);
+    G.last_images = 1;
+    return 0;
+}
+
+int ug_snapshot_tensor(void *ptr, uint32_t index, void *out, uint32_t bytes)
+{
+    Session *s = ptr;
+    if (!s || s != g_session || s->pipeline || !out || !bytes || bytes > 4u * 1024 * 1024) return 1003;
+    return ug_snapshot(index, out, bytes);
+}
+
+int ug_profile_control(void *ptr, uint32_t command, void *out, uint32_t bytes)
+{
+    Session *s = ptr;
+    if (!s || s != g_session || !out || (bytes != 130 * 8 && bytes != (UG_MAX_OP + 2) * 8) || command > 2) return 1003;
+    return ug_profile(command, out, bytes);
 }
 
 int ug_snapshot_images(uint32_t index, void *out, uint64_t bytes)

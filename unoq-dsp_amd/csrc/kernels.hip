@@ -18,7 +18,9 @@
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-static hipStream_t g_stream;
+static hipStream_t g_stream;      // compute (and the single-stream entry points)
+static hipStream_t g_copy[2];     // host transfers of the pipelined batch: in, out
+static hipEvent_t g_pipe_ev[8];   // pipeline hand-offs between the three streams
 static int g_ready;
 static int g_err;
 static hipEvent_t *g_events;
@@ -1079,7 +1081,8 @@ __global__ __launch_bounds__(256) void k_dw_win(DwWinArgs a)
         for (int i = 0; i < 4; i++) acc[t][i] = 0;
     // 5x5: one kernel row at a time keeps the register footprint small
     // enough for several waves per SIMD.
-#pragma unroll (KS > 4 ? 1 : KS)
+    constexpr int KU = KS > 4 ? 1 : KS;
+#pragma unroll KU
     for (int ky = 0; ky < KS; ky++) {
         const int r = tyi * S + ky;
         const int *row = W + (long)r * a.njq * jqs + cqi * 4;
@@ -1808,9 +1811,93 @@ extern "C" int uqk_init(void)
     int n = 0;
     UQK_TRY(hipGetDeviceCount(&n));
     if (n < 1) return (int)hipErrorNoDevice;
+    // All streams at the default priority.
     UQK_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+    UQK_TRY(hipStreamCreateWithFlags(&g_copy[0], hipStreamNonBlocking));
+    UQK_TRY(hipStreamCreateWithFlags(&g_copy[1], hipStreamNonBlocking));
+    for (int i = 0; i < 8; i++) UQK_TRY(hipEventCreateWithFlags(&g_pipe_ev[i], hipEventDisableTiming));
     g_ready = 1;
     return 0;
+}
+
+// Stream ids for the pipelined transfers: 0 compute, 1 host-to-device,
+// 2 device-to-host.
+static hipStream_t stream_of(int id) { return id == 0 ? g_stream : g_copy[id - 1]; }
+
+extern "C" int uqk_copy_on(int stream, void *dst, const void *src, size_t bytes, int to_device)
+{
+    if (bytes)
+        UQK_TRY(hipMemcpyAsync(dst, src, bytes, to_device ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost,
+                               stream_of(stream)));
+    return 0;
+}
+
+extern "C" int uqk_pipe_record(int event, int stream)
+{
+    if (event < 0 || event >= 8) return (int)hipErrorInvalidValue;
+    UQK_TRY(hipEventRecord(g_pipe_ev[event], stream_of(stream)));
+    return 0;
+}
+
+extern "C" int uqk_pipe_wait(int stream, int event)
+{
+    if (event < 0 || event >= 8) return (int)hipErrorInvalidValue;
+    UQK_TRY(hipStreamWaitEvent(stream_of(stream), g_pipe_ev[event], 0));
+    return 0;
+}
+
+extern "C" int uqk_sync_all(void)
+{
+    UQK_TRY(hipStreamSynchronize(g_copy[0]));
+    UQK_TRY(hipStreamSynchronize(g_stream));
+    UQK_TRY(hipStreamSynchronize(g_copy[1]));
+    return 0;
+}
+
+extern "C" void *uqk_host_alloc(size_t bytes)
+{
+    void *p = nullptr;
+    if (hipHostMalloc(&p, bytes ? bytes : 16, hipHostMallocDefault) != hipSuccess) return nullptr;
+    return p;
+}
+
+extern "C" void uqk_host_free(void *p)
+{
+    if (p) (void)hipHostFree(p);
+}
+
+// Whole-plan replay: capture what the host enqueues on the compute stream
+// into a graph, instantiate it, and launch it as one submission.
+extern "C" int uqk_capture_begin(void)
+{
+    UQK_TRY(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal));
+    return 0;
+}
+
+extern "C" int uqk_capture_end(void **exec)
+{
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t e = nullptr;
+    UQK_TRY(hipStreamEndCapture(g_stream, &graph));
+    const hipError_t rc = hipGraphInstantiate(&e, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (rc != hipSuccess) {
+        g_err = (int)rc;
+        return (int)rc;
+    }
+    *exec = (void *)e;
+    return 0;
+}
+
+extern "C" int uqk_graph_launch(void *exec)
+{
+    UQK_TRY(hipGraphLaunch((hipGraphExec_t)exec, g_stream));
+    return 0;
+}
+
+extern "C" void uqk_graph_destroy(void *exec)
+{
+    if (exec) (void)hipGraphExecDestroy((hipGraphExec_t)exec);
 }
 
 extern "C" void *uqk_malloc(size_t bytes)

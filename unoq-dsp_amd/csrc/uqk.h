@@ -66,6 +66,22 @@ int uqk_d2d_2d(void *dst, size_t dpitch, const void *src, size_t spitch, size_t 
 int uqk_sync(void);
 int uqk_last_error(void);
 
+/* Pipelined host transfers: stream 0 computes, 1 copies host -> device, 2
+ * device -> host (all at the default priority); events 0-7 hand work from
+ * one stream to another. */
+int uqk_copy_on(int stream, void *dst, const void *src, size_t bytes, int to_device);
+int uqk_pipe_record(int event, int stream);
+int uqk_pipe_wait(int stream, int event);
+int uqk_sync_all(void);
+void *uqk_host_alloc(size_t bytes);                   /* pinned (hipHostMalloc) */
+void uqk_host_free(void *p);
+
+/* Whole-plan graphs: capture the compute stream's submissions, replay them. */
+int uqk_capture_begin(void);
+int uqk_capture_end(void **exec);
+int uqk_graph_launch(void *exec);
+void uqk_graph_destroy(void *exec);
+
 int uqk_conv(const UQKSpatial *d, const void *x, void *y, uint32_t batches);
 int uqk_depthwise(const UQKSpatial *d, const void *x, void *y, uint32_t batches);
 int uqk_pool(const UQKSpatial *d, const void *x, void *y, uint32_t batches);

@@ -37,6 +37,15 @@ SIGNATURES = [
     ("ug_bundle_plan", C.c_int, [C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p), C.POINTER(C.c_uint32)]),
     ("ug_load_bundle", C.c_int, [C.c_void_p, C.c_uint64]),
     ("uq_sha256", None, [C.c_void_p, C.c_uint64, C.c_void_p]),
+    ("ug_run_batch_pipelined", C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint32]),
+    ("ug_host_alloc", C.c_void_p, [C.c_uint64]),
+    ("ug_host_free", C.c_int, [C.c_void_p]),
+    ("ug_open_mode", C.c_void_p, [C.c_void_p, C.c_uint32, C.c_int, C.POINTER(C.c_int)]),
+    ("ug_open", C.c_void_p, [C.c_void_p, C.c_uint32, C.POINTER(C.c_int)]),
+    ("ug_infer", C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32]),
+    ("ug_close", None, [C.c_void_p]),
+    ("ug_snapshot_tensor", C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32]),
+    ("ug_profile_control", C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32]),
 ]
 
 
@@ -100,6 +109,45 @@ class Graph:
         if rc:
             raise NativeError("ug_profile", rc)
         return counters
+
+
+class Session:
+    """The reference's HardwareSession contract (src/unoq_dsp/transport.py:
+    19-79) over the bridge ABI of this library: one model per process, calls
+    serialised, close idempotent, "mailbox" or "rpc" pipeline."""
+
+    def __init__(self, plan, pipeline="mailbox", lib=None):
+        if pipeline not in ("mailbox", "rpc"):
+            raise ValueError("pipeline must be mailbox or rpc")
+        self.lib = lib or open_library()
+        error = C.c_int()
+        buf = C.create_string_buffer(bytes(plan), len(plan))
+        self.handle = self.lib.ug_open_mode(buf, len(plan), int(pipeline == "mailbox"), C.byref(error))
+        if not self.handle:
+            raise NativeError("ug_open_mode", error.value & 0xffffffff)
+        self.input_bytes = self.lib.ug_input_bytes()
+        self.output_bytes = self.lib.ug_output_bytes()
+
+    def run(self, x):
+        if not self.handle:
+            raise RuntimeError("Session closed")
+        x = np.ascontiguousarray(x, dtype=np.int8).reshape(-1)
+        y = np.empty(self.output_bytes, np.int8)
+        rc = self.lib.ug_infer(self.handle, x.ctypes.data, x.nbytes, y.ctypes.data, y.nbytes)
+        if rc:
+            raise NativeError("ug_infer", rc)
+        return y
+
+    def close(self):
+        if self.handle:
+            self.lib.ug_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *args):
+        self.close()
 
 
 class DeviceBuffer:
