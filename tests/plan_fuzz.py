@@ -212,3 +212,46 @@ def random_plan(seed, max_ops=4, ops=None):
     elif tail == "copy":
         t = p.copy(t)
     return p.build(t)
+
+
+def conv_add_plan(seed):
+    """A residual block x -> conv -> {lut (the residual), 1x1 conv} -> add,
+    the add's operands in either order: the pattern the GPU library runs as
+    one launch (the add in the 1x1 conv's epilogue). Channel counts cover
+    16-multiples and byte tails; post tables, activations and both
+    requantisation ranges vary; the sum is sometimes used further on."""
+    rng = Rng(seed, 515151)
+    p = Plan(seed)
+    shape = (int(_pick(rng, [1, 1, 2])), int(rng.integers(1, 1, 10)[0]), int(rng.integers(1, 1, 10)[0]),
+             int(_pick(rng, [16, 32, 48, 64])))
+    t = p.input(shape, zp=int(rng.integers(1, -128, 127)[0]))
+    c = _pick(rng, [16, 32, 48, 64, 96])
+    q6 = int(rng.integers(1, 1, 200)[0])
+    h = p.conv(t, c, k=1, act=_pick(rng, ["none", "relu", "relu6"]), q6=q6, shift=(-12, -4))
+    residual = p.lut(h, _random_lut(p, rng))
+    lut = _random_lut(p, rng) if _pick(rng, [0, 0, 1]) else None
+    lo = int(rng.integers(1, -24, -1)[0])
+    shift = _pick(rng, [(lo, 3), (-12, -4), (-20, -1)])
+    y = p.conv(h, c, k=1, act=_pick(rng, ["none", "relu", "relu6"]), q6=q6, lut=lut, shift=shift,
+               zero_mult=_pick(rng, [0.0, 0.0, 0.3]), w_sigma=_pick(rng, [3, 40, 90]),
+               tail_weights=bool(_pick(rng, [0, 1])))
+    act = _pick(rng, ["none", "relu", "relu6"])
+    z = p.add(y, residual, act=act) if _pick(rng, [0, 1]) else p.add(residual, y, act=act)
+    if _pick(rng, [0, 1]):
+        z = p.conv(z, _pick(rng, [8, 16, 17]), k=1, shift=(-12, -4))
+    return p.build(z)
+
+
+def conv_add_bytes_plan(seed):
+    """As conv_add_plan with channel counts that are not multiples of 16 (the
+    epilogue's byte path)."""
+    rng = Rng(seed, 616161)
+    p = Plan(seed)
+    shape = (1, int(rng.integers(1, 1, 9)[0]), int(rng.integers(1, 1, 9)[0]), int(_pick(rng, [16, 32])))
+    t = p.input(shape, zp=int(rng.integers(1, -128, 127)[0]))
+    c = _pick(rng, [3, 5, 8, 12, 17, 20, 36])
+    h = p.lut(t, _random_lut(p, rng))
+    y = p.conv(h, c, k=1, act=_pick(rng, ["none", "relu"]), shift=(-12, -4))
+    r = p.conv(t, c, k=1, act="none", shift=(-12, -4))
+    z = p.add(y, r) if _pick(rng, [0, 1]) else p.add(r, y)
+    return p.build(z)

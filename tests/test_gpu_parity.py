@@ -10,7 +10,7 @@ import pytest
 
 import uq_plan as P
 import uq_workloads as W
-from plan_fuzz import ATTENTION_OPS, CONSTANT_OPS, random_plan
+from plan_fuzz import ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, random_plan
 from test_oracle_vs_reference import (BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, softmax_table_plan,
                                       transpose_plan)
 from refs import oracle_run
@@ -170,3 +170,66 @@ def test_bad_sizes_rejected(lib):
     assert lib.ug_run(x.ctypes.data, x.nbytes, y.ctypes.data, y.nbytes) == 22
     with pytest.raises(NativeError):
         g.run_batch(np.zeros(3 * g.input_bytes, np.int8), 2)
+
+
+@pytest.mark.parametrize("name,images", [("mnv4", 3), ("mnv4", 256)])
+def test_fused_bottleneck_opt_in(lib, monkeypatch, name, images):
+    """UQ_FUSE_BOTTLENECK=1 at load time runs 1x1 -> depthwise -> 1x1 (-> add)
+    groups as one launch; the bytes must not change, and snapshots of a group's
+    inner tensors are rebuilt from the group input."""
+    plan, _ = W.WORKLOADS[name]()
+    x = P.random_input(plan, images, 41)
+    monkeypatch.setenv("UQ_FUSE_BOTTLENECK", "1")
+    g = Graph(plan, lib)
+    y = g.run_batch(x, images)
+    ib, ob = g.input_bytes, g.output_bytes
+    for j in sorted({0, images // 2, images - 1}):
+        _assert_same(y[j * ob:(j + 1) * ob], _oracle(plan, x[j * ib:(j + 1) * ib], 1), f"fused {name} image {j}")
+    if images > 8:
+        return
+    recs = P.tensor_records(plan)
+    activations = [t for t, r in enumerate(recs) if not r[8]]
+    for t in activations[2:-1:5]:
+        nbytes = images * recs[t][1]
+        _, want = oracle_run(plan, x, images, P.output_bytes(plan), snap=t, snap_bytes=nbytes)
+        _assert_same(g.snapshot_images(t, nbytes), want, f"fused snapshot tensor {t}")
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_conv_add_fusion(lib, seed):
+    """A 1x1 conv followed by a residual add runs as one launch (the add in
+    the conv's epilogue): both operand orders, byte-tail channel counts."""
+    for plan, images in ((conv_add_plan(seed), 3), (conv_add_bytes_plan(seed), 2)):
+        x = P.random_input(plan, images, seed)
+        _assert_same(Graph(plan, lib).run_batch(x, images), _oracle(plan, x, images), f"conv+add plan {seed}")
+
+
+def _fused_conv_outputs(plan):
+    """Conv outputs read only by the add right after them (not written by a fused run)."""
+    ops = P.op_records(plan)
+    uses = {}
+    for o in ops:
+        for t in (o[1], o[2]):
+            uses[t] = uses.get(t, 0) + 1
+    return [c[3] for c, ad in zip(ops, ops[1:]) if c[0] == 14 and ad[0] == 18 and c[3] in (ad[1], ad[2])
+            and uses[c[3]] == 1]
+
+
+@pytest.mark.parametrize("name", ["mnv4", "fuzz"])
+def test_snapshot_of_fused_conv_output(lib, name):
+    """Snapshots of a fused conv's own output (never written by the fused
+    launch) are rebuilt from the group's inputs, and the run's output is
+    unchanged by the rebuild."""
+    plan = W.mnv4()[0] if name == "mnv4" else conv_add_plan(5)
+    images = 2
+    x = P.random_input(plan, images, 9)
+    g = Graph(plan, lib)
+    y = g.run_batch(x, images)
+    recs = P.tensor_records(plan)
+    targets = _fused_conv_outputs(plan)
+    assert targets
+    for t in targets[:4] + targets[-1:]:
+        nbytes = images * recs[t][1]
+        _, want = oracle_run(plan, x, images, P.output_bytes(plan), snap=t, snap_bytes=nbytes)
+        _assert_same(g.snapshot_images(t, nbytes), want, f"{name} snapshot tensor {t}")
+    _assert_same(g.run_batch(x, images), y, f"{name} rerun after snapshots")

@@ -16,6 +16,8 @@ their LiteRT expected values cannot run offline:
   * test_modern_ops.py:59-64    softmax widths 1..256 x five input scales
   * test_modern_ops.py:75-79    transposes of ranks 2, 3 and 4
   * test_modern_ops.py:87-94    bmm shapes x all four transpose flags
+Residual blocks (conv -> add, the pair the GPU library fuses) are fuzzed
+against the reference build too.
 """
 import struct
 from pathlib import Path
@@ -25,7 +27,7 @@ import pytest
 
 import uq_plan as P
 import uq_workloads as W
-from plan_fuzz import ATTENTION_OPS, CONSTANT_OPS, random_plan
+from plan_fuzz import ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, random_plan
 from refs import oracle_run, ref_plain, ref_release
 
 MODELS = Path("/root/reference/models")
@@ -119,6 +121,12 @@ def test_attention_plans_match_reference(seed):
 @pytest.mark.parametrize("seed", range(30))
 def test_constant_operand_plans_match_reference(seed):
     _check_plan(random_plan(8000 + seed, ops=CONSTANT_OPS), 3, seed)
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_conv_add_plans_match_reference(seed):
+    _check_plan(conv_add_plan(seed), 2, seed)
+    _check_plan(conv_add_bytes_plan(seed), 2, seed)
 
 
 def softmax_plan(width, beta_scale, rows=3, zp=-17):

@@ -31,6 +31,18 @@ typedef struct { uint32_t magic, version, nt, no, arena_bytes, input, output, re
 typedef struct { uint32_t offset, bytes, type, rank, d[4], flags, reserved[3]; } Tensor;
 typedef struct { uint32_t code, a, b, out, p[4]; } Op;
 
+/* A fused group (see find_groups): an inverted bottleneck run by one launch
+ * (kind 0), or a conv whose residual add runs in its epilogue (kind 1). */
+typedef struct {
+    int kind;
+    UQKIb desc;
+    UQKAdd add;                      /* kind 1; add.res is set per launch */
+    uint32_t res;                    /* kind 1: tensor of the add's other operand */
+    uint32_t first, nops, in, out;
+    const uint8_t *last_in;          /* input pointer of the last fused launch */
+    uint32_t last_images;            /* images of that launch, 0 if not run fused since */
+} Group;
+
 static struct {
     int ready, profile_enabled, stream_active, vision_only;
     Header h;
@@ -46,6 +58,14 @@ static struct {
     UQKSpatial sp[UG_MAX_OP];
     uint64_t ticks[UG_MAX_OP + 2];
     uint64_t generation;         /* bumped whenever device buffers move (graphs must be re-captured) */
+    /* Fused inverted-bottleneck groups: fuse_at[i] = group index + 1 when op i
+     * starts one. A group's inner tensors reach HBM only when a snapshot asks
+     * for them (materialize_group). */
+    uint16_t fuse_at[UG_MAX_OP];
+    uint16_t fuse_of_tensor[UG_MAX_T];   /* group index + 1 of an inner tensor */
+    uint8_t ext[UG_MAX_T];               /* G.ptr[t] is a caller buffer this run */
+    uint32_t ngroups;
+    Group groups[UG_MAX_OP / 2 + 1];
     uint8_t *pipe_in[2], *pipe_out[2]; /* device chunk buffers of the pipelined batch */
     uint64_t pipe_in_bytes, pipe_out_bytes;
 } G;
@@ -722,6 +742,159 @@ static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
     }
 }
 
+static int enqueue_op(uint32_t i, uint32_t images);
+
+/* Consumers of each activation tensor (operands a/b of every op, pack lists). */
+static void count_users(uint16_t *users)
+{
+    memset(users, 0, sizeof(uint16_t) * UG_MAX_T);
+    for (uint32_t i = 0; i < G.h.no; i++) {
+        const Op *o = G.ops + i;
+        users[o->a]++;
+        if (o->b != o->a) users[o->b]++;
+        if (o->code == 19) {
+            const Tensor *lt = G.ts + o->b;
+            const uint32_t *list = (const uint32_t *)(G.arena + lt->offset);
+            for (uint32_t j = 0; j < lt->bytes / 4; j++) users[list[j]]++;
+        }
+    }
+}
+
+static int pointwise_conv(uint32_t i)
+{
+    const Op *o = G.ops + i;
+    return o->code == 14 && G.sp[i].mode == UQK_PW && G.sp[i].kh == 1 && G.sp[i].kw == 1;
+}
+
+/* Fusable inverted bottlenecks: a 1x1 conv whose output feeds only a stride-1
+ * depthwise (window form, same map size) whose output feeds only a 1x1 conv,
+ * optionally followed by an add of that conv's output and the block input.
+ * Inner tensors must be single-use activations, not the plan output; the map
+ * must be one image per plan image (d0 == 1) and fit one workgroup's LDS.
+ *
+ * Off unless UQ_FUSE_BOTTLENECK=1 at load time: at batch 256 the fused kernel
+ * (one image per workgroup, phases separated by barriers) measures slower than
+ * the three separate launches, whose intermediate traffic costs little HBM
+ * time. The results are identical either way. */
+/* Conv + residual add: a conv run by k_conv whose output is used once, by
+ * the next op, an add (op 18) of equal-sized operands; neither the conv
+ * output nor anything else but the add's output is observable, so the add
+ * can run in the conv's epilogue. */
+static int find_conv_add(uint32_t i, const uint16_t *users)
+{
+    const Op *c = G.ops + i, *ad = G.ops + i + 1;
+    if (c->code != 14 || ad->code != 18 || !uqk_conv_add_ok(G.sp + i)) return 0;
+    const uint32_t t = c->out;
+    if (users[t] != 1 || t == G.h.output || (ad->a != t && ad->b != t) || ad->a == ad->b) return 0;
+    const uint32_t res = ad->a == t ? ad->b : ad->a;
+    if (G.ts[res].bytes != G.ts[t].bytes || G.ts[ad->out].bytes != G.ts[t].bytes) return 0;
+    if (G.ts[res].flags && !G.bcast[res]) return 0;
+    Group *g = &G.groups[G.ngroups];
+    memset(g, 0, sizeof *g);
+    g->kind = 1;
+    const int32_t *q = (const int32_t *)(G.arena + G.ts[ad->p[0]].offset);
+    g->add.tables = G.dev_arena + G.ts[ad->p[0]].offset + 8 * 4;
+    g->add.m = q[0]; g->add.s = q[1]; g->add.yz = q[2]; g->add.lo = q[3]; g->add.hi = q[4];
+    g->add.conv_is_a = ad->a == t;
+    g->res = res;
+    g->first = i;
+    g->nops = 2;
+    g->in = c->a;
+    g->out = ad->out;
+    G.fuse_at[i] = (uint16_t)(G.ngroups + 1);
+    G.fuse_of_tensor[t] = (uint16_t)(G.ngroups + 1);
+    G.ngroups++;
+    return 1;
+}
+
+static uint32_t find_bottleneck(uint32_t i, const uint16_t *users)
+{
+    if (i + 2 >= G.h.no) return 0;
+    const Op *e = G.ops + i, *d = G.ops + i + 1, *p = G.ops + i + 2;
+    if (!pointwise_conv(i) || d->code != 15 || !pointwise_conv(i + 2)) return 0;
+    const Tensor *x = G.ts + e->a;
+    const UQKSpatial *se = G.sp + i, *sd = G.sp + i + 1, *sp = G.sp + i + 2;
+    if (x->flags || x->rank != 4 || x->d[0] != 1 || e->a == G.h.input) return 0;
+    if (d->a != e->out || p->a != d->out || !sd->dwwin || sd->sh != 1 || sd->sw != 1) return 0;
+    if (sd->oh != se->oh || sd->ow != se->ow || sd->oc != se->oc || sp->ic != se->oc) return 0;
+    if (users[e->out] != 1 || users[d->out] != 1 || e->out == G.h.output || d->out == G.h.output) return 0;
+    if (se->ic % 16 || se->oc % 16 || sp->oc % 16) return 0;
+    const int P = se->oh * se->ow;
+    const size_t lds = uqk_ib_lds(P, se->ic, se->oc, sp->oc, sd->kh, NULL);
+    if (!lds || lds > 163840) return 0;
+    Group *g = &G.groups[G.ngroups];
+    memset(g, 0, sizeof *g);
+    UQKIb *f = &g->desc;
+    f->P = P; f->H = se->oh; f->W = se->ow; f->Cin = se->ic; f->Ce = se->oc; f->Cout = sp->oc;
+    f->ks = sd->kh; f->pt = sd->pt; f->pl = sd->pl;
+    f->we = se->w; f->epi_e = se->epi; f->lut_e = se->lut; f->kpe = se->kpad;
+    f->e_mode = (se->hi_shift ? 1 : 0) | (se->corr ? 2 : 0); f->e_yz = se->yz; f->e_lo = se->lo; f->e_hi = se->hi;
+    f->dww = sd->wdot; f->epi_d = sd->epi; f->lut_d = sd->lut;
+    f->d_mode = (sd->hi_shift ? 1 : 0) | (sd->corr ? 2 : 0); f->d_yz = sd->yz; f->d_lo = sd->lo; f->d_hi = sd->hi;
+    f->d_xz = sd->xz;
+    f->wp = sp->w; f->epi_p = sp->epi; f->lut_p = sp->lut; f->kpp = sp->kpad;
+    f->p_mode = (sp->hi_shift ? 1 : 0) | (sp->corr ? 2 : 0); f->p_yz = sp->yz; f->p_lo = sp->lo; f->p_hi = sp->hi;
+    g->first = i;
+    g->nops = 3;
+    g->in = e->a;
+    g->out = p->out;
+    if (i + 3 < G.h.no) {
+        const Op *ad = G.ops + i + 3;
+        const int ordered = ad->a == e->a && ad->b == p->out, swapped = ad->a == p->out && ad->b == e->a;
+        if (ad->code == 18 && (ordered || swapped) && users[p->out] == 1 && p->out != G.h.output &&
+            se->ic == sp->oc) {
+            const int32_t *q = (const int32_t *)(G.arena + G.ts[ad->p[0]].offset);
+            f->has_add = 1;
+            f->add_x_first = ordered;
+            f->add_tab = G.dev_arena + G.ts[ad->p[0]].offset + 8 * 4;
+            f->a_m = q[0]; f->a_s = q[1]; f->a_yz = q[2]; f->a_lo = q[3]; f->a_hi = q[4];
+            g->nops = 4;
+            g->out = ad->out;
+        }
+    }
+    G.fuse_at[i] = (uint16_t)(G.ngroups + 1);
+    G.fuse_of_tensor[e->out] = G.fuse_of_tensor[d->out] = (uint16_t)(G.ngroups + 1);
+    if (g->nops == 4) G.fuse_of_tensor[p->out] = (uint16_t)(G.ngroups + 1);
+    G.ngroups++;
+    return g->nops;
+}
+
+static void find_groups(void)
+{
+    static uint16_t users[UG_MAX_T];
+    memset(G.fuse_at, 0, sizeof G.fuse_at);
+    memset(G.fuse_of_tensor, 0, sizeof G.fuse_of_tensor);
+    G.ngroups = 0;
+    count_users(users);
+    const char *env = getenv("UQ_FUSE_BOTTLENECK");
+    const int bottleneck = env && !strcmp(env, "1");
+    for (uint32_t i = 0; i + 1 < G.h.no; i++) {
+        uint32_t n = bottleneck ? find_bottleneck(i, users) : 0;
+        if (!n && find_conv_add(i, users)) n = 2;
+        if (n) i += n - 1;
+    }
+}
+
+/* Write a fused group's inner tensors after a fused run (for snapshots): its
+ * ops again, one by one, from the input the fused launch read, into the
+ * library's own buffers. */
+static int materialize_group(uint32_t t)
+{
+    const uint32_t gi = G.fuse_of_tensor[t];
+    if (!gi) return 0;
+    Group *g = &G.groups[gi - 1];
+    if (!g->last_images) return 0;
+    uint8_t *saved_in = G.ptr[g->in];
+    G.ptr[g->in] = (uint8_t *)g->last_in;
+    for (uint32_t k = 0; k < g->nops; k++) G.ptr[G.ops[g->first + k].out] = G.act[G.ops[g->first + k].out];
+    int rc = 0;
+    for (uint32_t k = 0; k < g->nops && !rc; k++) rc = enqueue_op(g->first + k, g->last_images);
+    G.ptr[g->in] = saved_in;
+    if (!rc) rc = uqk_sync();
+    g->last_images = 0;
+    return rc ? 24 : 0;
+}
+
 static int prepare_device(void)
 {
     if (uqk_init()) return 24;
@@ -744,6 +917,7 @@ static int prepare_device(void)
         const Op *o = G.ops + i;
         if (o->code == 14 || o->code == 15 || o->code == 16) prepare_spatial(i, layouts + i, host_pool);
     }
+    find_groups();
     int rc = uqk_h2d(G.dev_arena, G.arena, G.h.arena_bytes);
     if (!rc) rc = uqk_h2d(G.dev_prep, host_pool, at + 256);
     if (!rc) rc = uqk_sync();
@@ -815,10 +989,45 @@ static int ensure_capacity(uint32_t images)
 
 /* Enqueue every op of the plan for `images` stacked images on the library
  * stream. Tensor addresses come from G.ptr. */
+/* Enqueue every op of the plan for `images` stacked images on the library
+ * stream, launching fused groups in place of their ops (not while per-op
+ * profiling is on, and not on a caller's input buffer). */
 static int enqueue_ops(uint32_t images)
 {
-    const uint8_t *A = G.arena;
     for (uint32_t i = 0; i < G.h.no; i++) {
+        const uint32_t g = G.fuse_at[i];
+        /* A group runs fused only when the buffers it reads are the library's
+         * own, which still hold the same bytes if a snapshot later asks for
+         * an inner tensor (materialize_group). */
+        if (g && !G.profile_enabled && !G.ext[G.groups[g - 1].in] &&
+            (G.groups[g - 1].kind == 0 || !G.ext[G.groups[g - 1].res])) {
+            Group *grp = &G.groups[g - 1];
+            int rc;
+            if (grp->kind == 0) {
+                rc = uqk_ib(&grp->desc, G.ptr[grp->in], G.ptr[grp->out], images);
+            } else {
+                grp->add.res = G.ptr[grp->res];
+                rc = uqk_conv_add(G.sp + i, G.ptr[grp->in], G.ptr[grp->out], images * G.ts[G.ops[i].a].d[0],
+                                  &grp->add);
+            }
+            if (rc) return rc;
+            grp->last_in = G.ptr[grp->in];
+            grp->last_images = images;
+            i += grp->nops - 1;
+            continue;
+        }
+        if (g) G.groups[g - 1].last_images = 0;
+        int rc = enqueue_op(i, images);
+        if (rc) return rc;
+    }
+    if (G.profile_enabled) return uqk_record(G.h.no);
+    return 0;
+}
+
+static int enqueue_op(uint32_t i, uint32_t images)
+{
+    const uint8_t *A = G.arena;
+    {
         const Op *o = G.ops + i;
         const Tensor *a = G.ts + o->a, *b = G.ts + o->b, *z = G.ts + o->out;
         void *zp = G.ptr[o->out];
@@ -843,8 +1052,11 @@ static int enqueue_ops(uint32_t images)
         case 5:
             /* Every tensor is written once (graph.c:72 forbids redefinition),
              * so an internal copy can alias its source instead of moving bytes. */
-            if (G.ptr[o->out] == G.act[o->out]) G.ptr[o->out] = (uint8_t *)G.ptr[o->a];
-            else rc = uqk_d2d(zp, ap, (size_t)images * z->bytes);
+            if (G.ptr[o->out] == G.act[o->out]) {
+                G.ptr[o->out] = (uint8_t *)G.ptr[o->a];
+                G.ext[o->out] = G.ext[o->a];
+            } else
+                rc = uqk_d2d(zp, ap, (size_t)images * z->bytes);
             break;
         case 22: rc = uqk_lut(ap, zp, (uint64_t)images * a->bytes, bp, a->type == 3 ? 128u : 0u); break;
         case 10: rc = uqk_permute(ap, zp, images, a->rank, a->d, o->p, width(a->type)); break;
@@ -913,16 +1125,23 @@ static int enqueue_ops(uint32_t images)
         }
         if (rc) return rc;
     }
-    if (G.profile_enabled) return uqk_record(G.h.no);
     return 0;
 }
 
 static void bind_pointers(const void *d_in, void *d_out)
 {
-    for (uint32_t t = 0; t < G.h.nt; t++)
+    for (uint32_t t = 0; t < G.h.nt; t++) {
         G.ptr[t] = G.ts[t].flags && !G.bcast[t] ? G.dev_arena + G.ts[t].offset : G.act[t];
-    if (d_in) G.ptr[G.h.input] = (uint8_t *)d_in;
-    if (d_out && G.h.output != G.h.input && !G.ts[G.h.output].flags) G.ptr[G.h.output] = (uint8_t *)d_out;
+        G.ext[t] = 0;
+    }
+    if (d_in) {
+        G.ptr[G.h.input] = (uint8_t *)d_in;
+        G.ext[G.h.input] = 1;
+    }
+    if (d_out && G.h.output != G.h.input && !G.ts[G.h.output].flags) {
+        G.ptr[G.h.output] = (uint8_t *)d_out;
+        G.ext[G.h.output] = 1;
+    }
 }
 
 /* Copy the output tensor to a caller buffer when it was not produced there. */
@@ -1225,6 +1444,7 @@ int ug_snapshot_images(uint32_t index, void *out, uint64_t bytes)
         return 0;
     }
     if (!G.last_images || bytes != (uint64_t)G.last_images * t->bytes) return 22;
+    if (materialize_group(index)) return fail(24);
     if (uqk_d2h(out, G.ptr[index], bytes) || uqk_sync()) return fail(24);
     return 0;
 }
@@ -1241,6 +1461,7 @@ int ug_snapshot(uint32_t index, void *out, uint32_t bytes)
         memcpy(out, G.arena + t->offset, bytes); /* arena contents before any run */
         return 0;
     }
+    if (materialize_group(index)) return fail(24);
     if (uqk_d2h(out, G.ptr[index], bytes) || uqk_sync()) return fail(24);
     return 0;
 }

@@ -116,6 +116,10 @@ struct ConvArgs {
     int kw, dw, taps;
     int images, segs, row_groups, kw_magic, stem_rows;   // stem grid, tap decomposition, staged rows
     int tiles, cols, rows_max;
+    // Fused residual add (k_conv only; res == nullptr when there is none).
+    const int8_t *res;
+    const int *add_tab;
+    int add_m, add_s, add_yz, add_lo, add_hi, add_conv_a;
 };
 
 template <int MODE>
@@ -228,6 +232,37 @@ __device__ __forceinline__ void stage_consts(const ConvArgs &a, int n0, int4 *ep
     if (a.lut && threadIdx.x < 64) ((int *)lut_s)[threadIdx.x] = ((const int *)a.lut)[threadIdx.x];
 }
 
+// The same constants in two halves for kernels whose operand loads are in
+// flight at that point: consts_load issues the loads into registers (one
+// record half and one table word per thread at most), consts_store
+// writes them to LDS later, so no wait for them stalls the operand prefetch.
+struct ConstRegs {
+    int4 e;
+    int l;
+};
+
+template <int NT>
+__device__ __forceinline__ ConstRegs consts_load(const ConvArgs &a, int n0)
+{
+    static_assert(2 * NT * 16 <= 256, "one record half per thread");
+    ConstRegs r = {{0, 0, 0, 0}, 0};
+    const int t = threadIdx.x;
+    if (t < 2 * NT * 16) {
+        const int col = n0 + (t >> 1);
+        r.e = a.epi[2 * (col < a.oc ? col : 0) + (t & 1)];
+    }
+    if (a.lut && t < 64) r.l = ((const int *)a.lut)[t];
+    return r;
+}
+
+template <int NT>
+__device__ __forceinline__ void consts_store(const ConvArgs &a, const ConstRegs &r, int4 *epi_s, int8_t *lut_s)
+{
+    const int t = threadIdx.x;
+    if (t < 2 * NT * 16) epi_s[t] = r.e;
+    if (a.lut && t < 64) ((int *)lut_s)[t] = r.l;
+}
+
 // Requantise a wave's RB*16 x NT*16 tile and store the valid rows
 // [row_base, row_limit). The MFMA result gives a lane one channel (lane & 15)
 // of four consecutive rows; the four bytes are packed into a word, and a 4x4
@@ -235,9 +270,47 @@ __device__ __forceinline__ void stage_consts(const ConvArgs &a, int n0, int4 *ep
 // v_perm) turns that into one row x four channels per lane, stored as one
 // dword. Needs OC % 4 == 0 (so a quad's channels are all valid or all not);
 // other widths take byte stores.
+// The residual add of op 18 on one word of four output bytes y and four
+// residual bytes r: s = ta[first + 128] + tb[second + 128], then
+// clamp(uq_scale(s, m, shift) + yz, lo, hi), first being the conv byte when
+// the conv output is the add's operand a.
+__device__ __forceinline__ int add_word(const ConvArgs &a, const int *tab, int y, int r)
+{
+    const int wa = a.add_conv_a ? y : r, wb = a.add_conv_a ? r : y;
+    int z[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int s1 = tab[sbyte(wa, j) + 128] + tab[256 + sbyte(wb, j) + 128];
+        z[j] = min(max(uq_scale(s1, a.add_m, a.add_s) + a.add_yz, a.add_lo), a.add_hi);
+    }
+    return pack4(z[0], z[1], z[2], z[3]);
+}
+
+// Residual words for a fused add, read before the K loop so that their
+// latency hides behind it: the word of lane's transposed output position,
+// row (rb*16 + 4*(lane >> 4) + (lane & 3)), channels n0 + nt*16 +
+// (lane & 12) .. + 3. Used when OC % 4 == 0 (otherwise the epilogue's byte
+// path reads the residual itself).
+template <int RB, int NT>
+__device__ __forceinline__ void load_residual(const ConvArgs &a, int (&rw)[RB][NT], long row_base, long row_limit,
+                                              int n0, int lane)
+{
+    const bool words = a.res && (a.oc & 3) == 0;
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+        const long row = row_base + rb * 16 + (lane >> 4) * 4 + (lane & 3);
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int c = n0 + nt * 16 + (lane & 12);
+            rw[rb][nt] = words && row < row_limit && c < a.oc ? *(const int *)(a.res + row * a.oc + c) : 0;
+        }
+    }
+}
+
 template <int RB, int NT, bool HI, bool CORR>
 __device__ __forceinline__ void conv_store(const ConvArgs &a, const v4i (&acc)[RB][NT], int8_t *stage, int n0, int lane,
-                                           long row_base, long row_limit, const int4 *epi_s, const int8_t *lut_s)
+                                           long row_base, long row_limit, const int4 *epi_s, const int8_t *lut_s,
+                                           const int *add_s, const int (&rw)[RB][NT])
 {
     constexpr int R = RB * 16;
     constexpr int BN = NT * 16;
@@ -258,7 +331,8 @@ __device__ __forceinline__ void conv_store(const ConvArgs &a, const v4i (&acc)[R
                 for (int i = 0; i < 4; i++) v[i] = lut_s[v[i] + 128];
             }
             if (words) {
-                const int t = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
+                int t = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
+                if (add_s) t = add_word(a, add_s, t, rw[rb][nt]);
                 *(int *)(stage + (rb * 16 + lg * 4 + (lane & 3)) * STRIDE + nt * 16 + (lr & ~3)) = t;
             } else {
 #pragma unroll
@@ -280,8 +354,94 @@ __device__ __forceinline__ void conv_store(const ConvArgs &a, const v4i (&acc)[R
         for (int c = lane; c < R * ncols; c += 64) {
             const int r = c / ncols, cc = c - r * ncols;
             const long row = row_base + r;
-            if (row < row_limit) a.y[row * a.oc + n0 + cc] = stage[r * STRIDE + cc];
+            if (row < row_limit) {
+                const long at = row * a.oc + n0 + cc;
+                int v = stage[r * STRIDE + cc];
+                if (add_s && !words) v = add_word(a, add_s, v, a.res[at]);
+                a.y[at] = (int8_t)v;
+            }
         }
+    }
+}
+
+// 4x4 transpose of 16-lane rows across four registers: afterwards row j of
+// r[q] holds what row q of r[j] held. One v_permlane32_swap per register pair
+// exchanges the upper half of the first with the lower half of the second;
+// one v_permlane16_swap exchanges the odd rows of the first with the even
+// rows of the second.
+__device__ __forceinline__ void rows_transpose4(int (&r)[4])
+{
+    auto s02 = __builtin_amdgcn_permlane32_swap(r[0], r[2], false, false);
+    auto s13 = __builtin_amdgcn_permlane32_swap(r[1], r[3], false, false);
+    auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+    auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+    r[0] = (int)s01[0]; r[1] = (int)s01[1]; r[2] = (int)s23[0]; r[3] = (int)s23[1];
+}
+
+// Requantise and store a wave's tile computed with the channels as the MFMA
+// rows (weights in the A operand, pixels in B): a lane holds channels
+// nt*16 + 4*(lane >> 4) + i (i = 0..3) of pixel rb*16 + (lane & 15), packed
+// into one word per (rb, nt). Per channel tile, the words of four row blocks
+// go through rows_transpose4, after which row j of the wave holds all 16
+// channels of one pixel of row block rb0 + j: one 16-byte store per lane, no
+// LDS round trip. Only one tile's four channel records and four words are
+// live at a time.
+template <int RB, int NT, bool HI, bool CORR>
+__device__ __forceinline__ void conv_store_direct(const ConvArgs &a, const v4i (&acc)[RB][NT], int n0, int lane,
+                                                  long row_base, long row_limit, const int4 *epi_s,
+                                                  const int8_t *lut_s)
+{
+    static_assert(RB % 4 == 0, "row blocks go through the transpose in fours");
+    const int lr = lane & 15, lg = lane >> 4;
+    const bool lut = a.lut != nullptr;
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int cb = n0 + nt * 16;
+        Epi e[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) e[i] = load_epi(epi_s, nt * 16 + 4 * lg + i);
+#pragma unroll
+        for (int rb0 = 0; rb0 < RB; rb0 += 4) {
+            int r[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                int v[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[rb0 + q][nt][i], e[i], a.yz, a.lo, a.hi);
+                if (lut) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) v[i] = lut_s[v[i] + 128];
+                }
+                r[q] = pack4(v[0], v[1], v[2], v[3]);
+            }
+            rows_transpose4(r);
+            const long row = row_base + (rb0 + lg) * 16 + lr;
+            if (row >= row_limit || cb >= a.oc) continue;
+            int8_t *dst = a.y + row * a.oc + cb;
+            if ((a.oc & 15) == 0) {
+                *(v4i *)dst = (v4i){r[0], r[1], r[2], r[3]};
+            } else {
+                const int rem = min(16, a.oc - cb);
+#pragma nounroll
+                for (int b = 0; b < rem; b++) {
+                    const int w = b < 4 ? r[0] : b < 8 ? r[1] : b < 12 ? r[2] : r[3];
+                    dst[b] = (int8_t)(w >> (8 * (b & 3)));
+                }
+            }
+        }
+    }
+}
+
+template <int RB, int NT>
+__device__ __forceinline__ void conv_epilogue_direct(const ConvArgs &a, const v4i (&acc)[RB][NT], int n0, int lane,
+                                                     long row_base, long row_limit, const int4 *epi_s,
+                                                     const int8_t *lut_s)
+{
+    switch (a.emode) {
+    case 0: conv_store_direct<RB, NT, false, false>(a, acc, n0, lane, row_base, row_limit, epi_s, lut_s); break;
+    case 1: conv_store_direct<RB, NT, true, false>(a, acc, n0, lane, row_base, row_limit, epi_s, lut_s); break;
+    case 2: conv_store_direct<RB, NT, false, true>(a, acc, n0, lane, row_base, row_limit, epi_s, lut_s); break;
+    default: conv_store_direct<RB, NT, true, true>(a, acc, n0, lane, row_base, row_limit, epi_s, lut_s); break;
     }
 }
 
@@ -289,14 +449,81 @@ __device__ __forceinline__ void conv_store(const ConvArgs &a, const v4i (&acc)[R
 template <int RB, int NT>
 __device__ __forceinline__ void conv_epilogue(const ConvArgs &a, const v4i (&acc)[RB][NT], int8_t *stage, int n0,
                                               int lane, long row_base, long row_limit, const int4 *epi_s,
-                                              const int8_t *lut_s)
+                                              const int8_t *lut_s, const int *add_s, const int (&rw)[RB][NT])
 {
     switch (a.emode) {
-    case 0: conv_store<RB, NT, false, false>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s); break;
-    case 1: conv_store<RB, NT, true, false>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s); break;
-    case 2: conv_store<RB, NT, false, true>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s); break;
-    default: conv_store<RB, NT, true, true>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s); break;
+    case 0: conv_store<RB, NT, false, false>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s, add_s, rw); break;
+    case 1: conv_store<RB, NT, true, false>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s, add_s, rw); break;
+    case 2: conv_store<RB, NT, false, true>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s, add_s, rw); break;
+    default: conv_store<RB, NT, true, true>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s, add_s, rw); break;
     }
+}
+
+// Without a fused add.
+template <int RB, int NT>
+__device__ __forceinline__ void conv_epilogue(const ConvArgs &a, const v4i (&acc)[RB][NT], int8_t *stage, int n0,
+                                              int lane, long row_base, long row_limit, const int4 *epi_s,
+                                              const int8_t *lut_s)
+{
+    const int rw[RB][NT] = {};
+    conv_epilogue<RB, NT>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s, nullptr, rw);
+}
+
+// Copy K bytes [kc0, kc0 + kn) of a block's NT*16 weight rows (row stride
+// kpad in the [oc_pad][kpad] matrix) to LDS with row stride wstride: 16-byte
+// loads in K order (whole lines when kn == kpad, the slice then being one
+// contiguous range), four per thread issued before the first LDS write.
+template <int NT>
+__device__ __forceinline__ void stage_weights(const int8_t *wslice, int kpad, int kc0, int kn, int wstride, int8_t *dst)
+{
+    const int cpr = kn >> 4, total = NT * 16 * cpr;
+    for (int c0 = threadIdx.x; c0 < total; c0 += 4 * 256) {
+        v4i v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int c = c0 + j * 256;
+            if (c < total) {
+                const int r = c / cpr, q = c - r * cpr;
+                v[j] = *(const v4i *)(wslice + (long)r * kpad + kc0 + q * 16);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int c = c0 + j * 256;
+            if (c < total) {
+                const int r = c / cpr, q = c - r * cpr;
+                *(v4i *)(dst + r * wstride + q * 16) = v[j];
+            }
+        }
+    }
+}
+
+// Operand ring depth of k_conv: as many K steps in flight as fit about 96
+// registers, a power of two in [2, 8].
+__host__ __device__ constexpr int conv_ring(int rb, int nt)
+{
+    return 96 / ((rb + nt) * 4) >= 8 ? 8 : 96 / ((rb + nt) * 4) >= 4 ? 4 : 2;
+}
+
+// K bytes of the block's weight slice staged in LDS at a time: all of kpad
+// when NT*16 rows of kpad + 16 bytes fit 48 KiB, else the largest multiple
+// of 64 * ring depth that fits (so every chunk starts on ring slot 0).
+__host__ __device__ inline int conv_wchunk(int kpad, int rb, int nt)
+{
+    const int rows = nt * 16, budget = 49152;
+    if (rows * (kpad + 16) <= budget) return kpad;
+    const int unit = 64 * conv_ring(rb, nt);
+    const int kc = (budget / rows - 16) / unit * unit;
+    return kc < unit ? unit : kc;
+}
+
+// Dynamic LDS of k_conv: the staged weight chunk, or the output stage that
+// reuses it after the K loop when that is larger.
+__host__ __device__ inline size_t conv_lds(int kpad, int rb, int nt)
+{
+    const size_t w = (size_t)nt * 16 * (conv_wchunk(kpad, rb, nt) + 16);
+    const size_t st = (size_t)4 * rb * 16 * (nt * 16 + 16);
+    return w > st ? w : st;
 }
 
 template <int RB, int NT, int MODE>
@@ -304,9 +531,11 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
 {
     constexpr int R = RB * 16;
     constexpr int STRIDE = NT * 16 + 16;
-    __shared__ __attribute__((aligned(16))) int8_t stage[4][R * STRIDE];
+    constexpr int P = conv_ring(RB, NT);
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     __shared__ __attribute__((aligned(4))) int8_t lut_s[256];
     __shared__ int4 epi_s[2 * NT * 16];
+    __shared__ int add_s[512];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;
@@ -335,43 +564,83 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
         }
     }
 
-    const int8_t *wrow = a.w + (long)(n0 + lr) * a.kpad + lg * 16;
+    // Pixel operand on a ring of P register slots: the loads of steps
+    // s + 1 .. s + P - 1 are in flight while step s multiplies. The block's
+    // weight slice (NT*16 rows, contiguous in the [oc_pad][kpad] matrix) is
+    // staged in LDS once per K chunk with full-line loads and read from there
+    // by all four waves; rows are padded by 16 bytes, so the 16 rows of a
+    // 16-byte fragment read fall in distinct banks.
     const int steps = a.kpad >> 6;
-    v4i A[RB], B[NT];
+    const int kc = conv_wchunk(a.kpad, RB, NT), wstride = kc + 16;
+    v4i A[P][RB];
 #pragma unroll
-    for (int rb = 0; rb < RB; rb++) A[rb] = gather16<MODE>(a, base[rb], iy0[rb], ix0[rb], valid[rb], lg * 16, xzw);
+    for (int p = 0; p < P; p++) {
+        if (p < steps) {
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) B[nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad);
-    stage_consts<NT>(a, n0, epi_s, lut_s);
+            for (int rb = 0; rb < RB; rb++)
+                A[p][rb] = gather16<MODE>(a, base[rb], iy0[rb], ix0[rb], valid[rb], p * 64 + lg * 16, xzw);
+        }
+    }
+    const ConstRegs consts = consts_load<NT>(a, n0);
+    int rw[RB][NT];
+    load_residual<RB, NT>(a, rw, row0, a.M, n0, lane);
     v4i acc[RB][NT];
 #pragma unroll
     for (int rb = 0; rb < RB; rb++)
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) acc[rb][nt] = (v4i){0, 0, 0, 0};
-    for (int s = 0; s < steps; s++) {
-        v4i An[RB], Bn[NT];
-        const bool more = s + 1 < steps;
-        if (more) {
-            const int k1 = (s + 1) * 64;
+    const int8_t *wslice = a.w + (long)n0 * a.kpad;
+    if (steps == 1) {
+        // One K step: the weight fragments straight from global memory (a
+        // staging round trip would only add a barrier).
+        const int8_t *wrow = wslice + (long)lr * a.kpad + lg * 16;
+        v4i B[NT];
 #pragma unroll
-            for (int rb = 0; rb < RB; rb++) An[rb] = gather16<MODE>(a, base[rb], iy0[rb], ix0[rb], valid[rb], k1 + lg * 16, xzw);
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) Bn[nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad + k1);
-        }
+        for (int nt = 0; nt < NT; nt++) B[nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad);
 #pragma unroll
         for (int nt = 0; nt < NT; nt++)
 #pragma unroll
             for (int rb = 0; rb < RB; rb++)
-                acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[rb], B[nt], acc[rb][nt], 0, 0, 0);
-        if (more) {
+                acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0][rb], B[nt], acc[rb][nt], 0, 0, 0);
+    }
+    for (int kc0 = 0; steps > 1 && kc0 < a.kpad; kc0 += kc) {
+        const int kn = min(kc, a.kpad - kc0);
+        if (kc0) __syncthreads();
+        stage_weights<NT>(wslice, a.kpad, kc0, kn, wstride, smem);
+        __syncthreads();
+        const int s_begin = kc0 >> 6, s_end = (kc0 + kn) >> 6;
+        const int8_t *wl = smem + lr * wstride + lg * 16;
+        for (int s0 = s_begin; s0 < s_end; s0 += P) {
 #pragma unroll
-            for (int rb = 0; rb < RB; rb++) A[rb] = An[rb];
+            for (int p = 0; p < P; p++) {
+                const int s = s0 + p;
+                if (s < s_end) {
+                    v4i B[NT];
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++) B[nt] = Bn[nt];
+                    for (int nt = 0; nt < NT; nt++) B[nt] = *(const v4i *)(wl + nt * 16 * wstride + (s - s_begin) * 64);
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                        for (int rb = 0; rb < RB; rb++)
+                            acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[p][rb], B[nt], acc[rb][nt], 0, 0, 0);
+                    if (s + P < steps) {
+                        const int k1 = (s + P) * 64;
+#pragma unroll
+                        for (int rb = 0; rb < RB; rb++)
+                            A[p][rb] = gather16<MODE>(a, base[rb], iy0[rb], ix0[rb], valid[rb], k1 + lg * 16, xzw);
+                    }
+                }
+            }
         }
     }
+    consts_store<NT>(a, consts, epi_s, lut_s);
+    if (a.res) {
+        add_s[threadIdx.x] = a.add_tab[threadIdx.x];
+        add_s[256 + threadIdx.x] = a.add_tab[256 + threadIdx.x];
+    }
     __syncthreads();
-    conv_epilogue<RB, NT>(a, acc, stage[wave], n0, lane, row0, a.M, epi_s, lut_s);
+    conv_epilogue<RB, NT>(a, acc, smem + wave * R * STRIDE, n0, lane, row0, a.M, epi_s, lut_s,
+                          a.res ? add_s : nullptr, rw);
 }
 
 // Spatial conv with the block's input rows staged in LDS. A block covers BM =
@@ -408,39 +677,53 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
 
     const int iy_lo = oy_a * a.sh - a.pt;
     const int8_t *xim = a.x + n * a.ih * a.iw * a.ic;
+    // Staging: each thread issues STAGE_U loads before its first LDS write,
+    // so a block waits for about one HBM latency, not one per staged row.
+    constexpr int STAGE_U = 4;
     if (!WORDS) {
         const int xzw = (a.xz & 0xff) * 0x01010101;
-        const int cpr = rowbytes >> 4;
-        for (int q = threadIdx.x; q < rows * cpr; q += 256) {
-            const int r = q / cpr, b = (q - r * cpr) << 4;
-            const int col = b / a.ic, c = b - col * a.ic;
-            const int iy = iy_lo + r, ix = col - a.pl;
-            v4i v = {xzw, xzw, xzw, xzw};
-            if (iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw) v = *(const v4i *)(xim + ((long)iy * a.iw + ix) * a.ic + c);
-            *(v4i *)(xt + r * rowbytes + b) = v;
+        const int cpr = rowbytes >> 4, total = rows * cpr;
+        for (int q0 = threadIdx.x; q0 < total; q0 += STAGE_U * 256) {
+            v4i v[STAGE_U];
+#pragma unroll
+            for (int j = 0; j < STAGE_U; j++) {
+                const int q = q0 + j * 256;
+                const int r = q / cpr, b = (q - r * cpr) << 4;
+                const int col = b / a.ic, c = b - col * a.ic;
+                const int iy = iy_lo + r, ix = col - a.pl;
+                v[j] = (v4i){xzw, xzw, xzw, xzw};
+                if (q < total && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw)
+                    v[j] = *(const v4i *)(xim + ((long)iy * a.iw + ix) * a.ic + c);
+            }
+#pragma unroll
+            for (int j = 0; j < STAGE_U; j++)
+                if (q0 + j * 256 < total) *(v4i *)(xt + (q0 + j * 256) * 16) = v[j];
         }
     } else {
-        // One staged row at a time (a block-uniform loop), one LDS word per
-        // thread and iteration: no division when a pixel is a single word.
-        const int wpp = a.icp >> 2, wpr = a.cols * wpp, xzb = a.xz & 0xff;
-        for (int r = 0; r < rows; r++) {
-            const int iy = iy_lo + r;
-            const bool rowin = iy >= 0 && iy < a.ih;
-            const int8_t *srow = xim + (long)(rowin ? iy : 0) * a.iw * a.ic;
-            int *drow = (int *)(xt + r * rowbytes);
-            for (int wi = threadIdx.x; wi < wpr; wi += 256) {
+        // One LDS word per item (a pixel's channels widened to icp bytes,
+        // bytes past IC zero, padding positions the zero point).
+        const int wpp = a.icp >> 2, wpr = a.cols * wpp, xzb = a.xz & 0xff, total = rows * wpr;
+        for (int q0 = threadIdx.x; q0 < total; q0 += STAGE_U * 256) {
+            int w[STAGE_U];
+#pragma unroll
+            for (int j = 0; j < STAGE_U; j++) {
+                const int q = q0 + j * 256;
+                const int r = q / wpr, wi = q - r * wpr;
                 const int col = wpp == 1 ? wi : wi / wpp, cw = wi - col * wpp;
-                const int ix = col - a.pl;
-                const bool in = rowin && ix >= 0 && ix < a.iw;
-                const int8_t *src = srow + (long)(in ? ix : 0) * a.ic + cw * 4;
+                const int iy = iy_lo + r, ix = col - a.pl;
+                const bool in = q < total && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
+                const int8_t *src = xim + (in ? ((long)iy * a.iw + ix) * a.ic : 0) + cw * 4;
                 int word = 0;
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int b = cw * 4 + j < a.ic ? (in ? (int)(uint8_t)src[j] : xzb) : 0;
-                    word |= b << (8 * j);
+                for (int k = 0; k < 4; k++) {
+                    const int b = cw * 4 + k < a.ic ? (in ? (int)(uint8_t)src[k] : xzb) : 0;
+                    word |= b << (8 * k);
                 }
-                drow[wi] = word;
+                w[j] = word;
             }
+#pragma unroll
+            for (int j = 0; j < STAGE_U; j++)
+                if (q0 + j * 256 < total) ((int *)xt)[q0 + j * 256] = w[j];
         }
     }
     for (int i = threadIdx.x; i < ndelta; i += 256) dl[i] = a.delta[i];
@@ -458,49 +741,75 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
         lbase[rb] = ((oy - oy_a) * a.sh * a.cols + ox * a.sw) * a.icp;
     }
 
+    // Weights on a ring of P register slots (the pixel operand comes from
+    // LDS): steps s + 1 .. s + P - 1 are in flight while step s multiplies.
+    // (Staging them in LDS as k_conv does costs these blocks occupancy: the
+    // pixel tile already holds most of the block's LDS.)
+    constexpr int P = 96 / (NT * 4) >= 8 ? 8 : 96 / (NT * 4) >= 4 ? 4 : 2;
     const int8_t *wrow = a.w + (long)(n0 + lr) * a.kpad + lg * 16;
     const int steps = a.kpad >> 6;
-    v4i B[NT];
+    v4i B[P][NT];
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) B[nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad);
+    for (int p = 0; p < P; p++) {
+        if (p < steps) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) B[p][nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad + p * 64);
+        }
+    }
     v4i acc[RB][NT];
 #pragma unroll
     for (int rb = 0; rb < RB; rb++)
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) acc[rb][nt] = (v4i){0, 0, 0, 0};
-    for (int s = 0; s < steps; s++) {
-        const int kg = s * 64 + lg * 16;
-        v4i Bn[NT];
-        const bool more = s + 1 < steps;
-        if (more) {
+    for (int s0 = 0; s0 < steps; s0 += P) {
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++) Bn[nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad + (s + 1) * 64);
-        }
-        v4i A[RB];
+        for (int p = 0; p < P; p++) {
+            const int s = s0 + p;
+            if (s >= steps) break;
+            const int kg = s * 64 + lg * 16;
+            // The K slice's LDS offsets are shared by the row blocks; reads
+            // are unconditional (every lbase is a valid pixel of the tile,
+            // slices past K read offset 0) and invalid rows or slices are
+            // zeroed afterwards, so no LDS round trip waits inside a branch.
+            v4i A[RB];
+            if (!WORDS) {
+                const bool kin = kg < a.K;
+                const int d = dl[kin ? kg >> 4 : 0];
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++) {
-            v4i v = {0, 0, 0, 0};
-            if (valid[rb] && kg < a.K) {
-                if (!WORDS) {
-                    v = *(const v4i *)(xt + lbase[rb] + dl[kg >> 4]);
-                } else {
-                    const int w0 = kg >> 2;
+                for (int rb = 0; rb < RB; rb++) {
+                    const v4i v = *(const v4i *)(xt + lbase[rb] + d);
+                    const bool use = kin && valid[rb];
+                    A[rb] = (v4i){use ? v[0] : 0, use ? v[1] : 0, use ? v[2] : 0, use ? v[3] : 0};
+                }
+            } else {
+                const int w0 = kg >> 2;
+                int d[4];
+                bool win[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    win[j] = kg < a.K && w0 + j < ndelta;
+                    d[j] = dl[win[j] ? w0 + j : 0];
+                }
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++) {
                     int r4[4];
 #pragma unroll
-                    for (int j = 0; j < 4; j++) r4[j] = w0 + j < ndelta ? *(const int *)(xt + lbase[rb] + dl[w0 + j]) : 0;
-                    v = (v4i){r4[0], r4[1], r4[2], r4[3]};
+                    for (int j = 0; j < 4; j++) {
+                        const int v = *(const int *)(xt + lbase[rb] + d[j]);
+                        r4[j] = win[j] && valid[rb] ? v : 0;
+                    }
+                    A[rb] = (v4i){r4[0], r4[1], r4[2], r4[3]};
                 }
             }
-            A[rb] = v;
-        }
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++)
+            for (int nt = 0; nt < NT; nt++)
 #pragma unroll
-            for (int rb = 0; rb < RB; rb++)
-                acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[rb], B[nt], acc[rb][nt], 0, 0, 0);
-        if (more) {
+                for (int rb = 0; rb < RB; rb++)
+                    acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[rb], B[p][nt], acc[rb][nt], 0, 0, 0);
+            if (s + P < steps) {
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++) B[nt] = Bn[nt];
+                for (int nt = 0; nt < NT; nt++) B[p][nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad + (s + P) * 64);
+            }
         }
     }
     const long img0 = n * a.ohw;
@@ -513,18 +822,18 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
 // output rows of one image; each wave covers a 16*RB-pixel segment of its
 // row, so the image, the row and every kernel row's input row are
 // wave-uniform. The input rows the block touches are copied into LDS as they
-// are (rows of IW*IC bytes, 16-byte loads). Lane l supplies the A operand of
-// pixel l & 15 of a row block, K slice l >> 4 = taps 4s .. 4s + 3: each tap
-// is the four bytes at the pixel's input position (two aligned LDS words and
-// a byte shift); the bytes past the channel count land on zero weights, and
-// padding positions use the zero-point word.
+// are (rows of IW*IC bytes, 16-byte loads). Lane l supplies the pixel
+// operand of pixel l & 15 of a row block, K slice l >> 4 = taps 4s .. 4s + 3:
+// each tap is the four bytes at the pixel's input position (two aligned LDS
+// words and a byte shift); the bytes past the channel count land on zero
+// weights, and padding positions use the zero-point word. The channels are
+// the MFMA's rows, so the requantised bytes leave straight from registers
+// (conv_store_direct).
 template <int RB, int NT>
 __global__ __launch_bounds__(256) void k_conv_stem(ConvArgs a)
 {
     constexpr int R = RB * 16;
-    constexpr int STRIDE = NT * 16 + 16;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-    __shared__ __attribute__((aligned(16))) int8_t stage[4][R * STRIDE];
     __shared__ __attribute__((aligned(4))) int8_t lut_s[256];
     __shared__ int4 epi_s[2 * NT * 16];
 
@@ -547,14 +856,26 @@ __global__ __launch_bounds__(256) void k_conv_stem(ConvArgs a)
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) B[nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad);
 
-    // Stage the rows (rows outside the image are never read).
-    const int chunks = rowbytes >> 4;
-    for (int r = 0; r < a.stem_rows; r++) {
-        const int iy = iy_base + r;
-        if ((unsigned)iy >= (unsigned)a.ih) continue;
-        const v4i *src = (const v4i *)(xim + (long)iy * rowbytes);
-        v4i *dst = (v4i *)(smem + r * rowbytes);
-        for (int c = threadIdx.x; c < chunks; c += 256) dst[c] = src[c];
+    // Stage the rows: they are contiguous in the image and in LDS, so chunk c
+    // is image byte iy_base * rowbytes + 16 c. Chunks of rows outside the
+    // image are skipped (never read). Four loads per thread are issued before
+    // the first LDS write.
+    {
+        const int total = a.stem_rows * (rowbytes >> 4);
+        const long g0 = (long)iy_base * rowbytes, gend = (long)a.ih * rowbytes;
+        for (int c0 = threadIdx.x; c0 < total; c0 += 4 * 256) {
+            v4i v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const long g = g0 + (long)(c0 + j * 256) * 16;
+                if (c0 + j * 256 < total && g >= 0 && g < gend) v[j] = *(const v4i *)(xim + g);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const long g = g0 + (long)(c0 + j * 256) * 16;
+                if (c0 + j * 256 < total && g >= 0 && g < gend) ((v4i *)smem)[c0 + j * 256] = v[j];
+            }
+        }
     }
     stage_consts<NT>(a, n0, epi_s, lut_s);
 
@@ -577,30 +898,32 @@ __global__ __launch_bounds__(256) void k_conv_stem(ConvArgs a)
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
         const int ox = ox0 + rb * 16 + lr;
+        // Branch-free: every lane reads (offset 0 for padding taps) and
+        // selects afterwards, so all the wave's LDS reads are in flight at
+        // once instead of one round trip per tap.
         int words[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int ix = ox * a.sw + dx[j];
-            int v = xzw;
-            if (tap_ok[j] && ox < a.ow && (unsigned)ix < (unsigned)a.iw) {
-                const int off = ry[j] + ix * a.ic;
-                const int lo = lw[off >> 2], hi = lw[(off >> 2) + 1];
-                v = (int)__builtin_amdgcn_alignbyte((unsigned)hi, (unsigned)lo, (unsigned)(off & 3));
-            }
-            words[j] = v;
+            const bool ok = tap_ok[j] && ox < a.ow && (unsigned)ix < (unsigned)a.iw;
+            const int off = ok ? ry[j] + ix * a.ic : 0;
+            const int lo = lw[off >> 2], hi = lw[(off >> 2) + 1];
+            const int v = (int)__builtin_amdgcn_alignbyte((unsigned)hi, (unsigned)lo, (unsigned)(off & 3));
+            words[j] = ok ? v : xzw;
         }
         A[rb] = (v4i){words[0], words[1], words[2], words[3]};
     }
+    // Channels as the MFMA rows (weights in A), pixels as its columns.
     v4i acc[RB][NT];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++)
 #pragma unroll
         for (int rb = 0; rb < RB; rb++)
-            acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[rb], B[nt], (v4i){0, 0, 0, 0}, 0, 0, 0);
-    // Rows of M for this wave: its output row, pixels ox0 .. min(ox0 + R, ow).
+            acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(B[nt], A[rb], (v4i){0, 0, 0, 0}, 0, 0, 0);
+    // Output pixels of this wave: its output row, ox0 .. min(ox0 + R, ow).
     const long rbase = ((long)n * a.oh + oy) * a.ow + ox0;
     const long rlimit = row_ok ? ((long)n * a.oh + oy) * a.ow + a.ow : rbase;
-    conv_epilogue<RB, NT>(a, acc, stage[wave], n0, lane, rbase, rlimit, epi_s, lut_s);
+    conv_epilogue_direct<RB, NT>(a, acc, n0, lane, rbase, rlimit, epi_s, lut_s);
 }
 
 // Dynamic LDS of k_conv_stem (staged input rows plus one word of slack for
@@ -620,10 +943,10 @@ template <int RB, int NT>
 static void launch_conv_mode(int mode, const ConvArgs &a, dim3 grid, size_t lds)
 {
     switch (mode) {
-    case UQK_PW: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW>), grid, dim3(256), 0, g_stream, a); break;
-    case UQK_G16: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G16>), grid, dim3(256), 0, g_stream, a); break;
-    case UQK_G4: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G4>), grid, dim3(256), 0, g_stream, a); break;
-    case UQK_G1: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G1>), grid, dim3(256), 0, g_stream, a); break;
+    case UQK_PW: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW>), grid, dim3(256), conv_lds(a.kpad, RB, NT), g_stream, a); break;
+    case UQK_G16: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G16>), grid, dim3(256), conv_lds(a.kpad, RB, NT), g_stream, a); break;
+    case UQK_G4: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G4>), grid, dim3(256), conv_lds(a.kpad, RB, NT), g_stream, a); break;
+    case UQK_G1: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G1>), grid, dim3(256), conv_lds(a.kpad, RB, NT), g_stream, a); break;
     case UQK_ROWS16: hipLaunchKernelGGL((k_conv_rows<RB, NT, false>), grid, dim3(256), lds, g_stream, a); break;
     default: hipLaunchKernelGGL((k_conv_rows<RB, NT, true>), grid, dim3(256), lds, g_stream, a); break;
     }
@@ -670,9 +993,31 @@ extern "C" size_t uqk_conv_rows_lds(const UQKSpatial *d, int rb)
            (size_t)4 * 16 * rb * (16 * d->nt + 16);
 }
 
+static int conv_launch(const UQKSpatial *d, const void *x, void *y, uint32_t batches, const UQKAdd *add);
+
 extern "C" int uqk_conv(const UQKSpatial *d, const void *x, void *y, uint32_t batches)
 {
+    return conv_launch(d, x, y, batches, nullptr);
+}
+
+extern "C" int uqk_conv_add_ok(const UQKSpatial *d)
+{
+    return d->mode == UQK_PW || d->mode == UQK_G16 || d->mode == UQK_G4 || d->mode == UQK_G1;
+}
+
+extern "C" int uqk_conv_add(const UQKSpatial *d, const void *x, void *y, uint32_t batches, const UQKAdd *add)
+{
+    if (!uqk_conv_add_ok(d) || !add || !add->res || !add->tables) return (int)hipErrorInvalidValue;
+    return conv_launch(d, x, y, batches, add);
+}
+
+static int conv_launch(const UQKSpatial *d, const void *x, void *y, uint32_t batches, const UQKAdd *add)
+{
     ConvArgs a;
+    a.res = add ? (const int8_t *)add->res : nullptr;
+    a.add_tab = add ? (const int *)add->tables : nullptr;
+    a.add_m = add ? add->m : 0; a.add_s = add ? add->s : 0; a.add_yz = add ? add->yz : 0;
+    a.add_lo = add ? add->lo : 0; a.add_hi = add ? add->hi : 0; a.add_conv_a = add ? add->conv_is_a : 0;
     a.x = (const int8_t *)x;
     a.y = (int8_t *)y;
     a.w = (const int8_t *)d->w;
@@ -1204,6 +1549,270 @@ static int launch_dw_win(const UQKSpatial *d, const void *x, void *y, uint32_t b
     else if (d->sh == 1) UQK_DWW(5, 1);
     else UQK_DWW(5, 2);
 #undef UQK_DWW
+    UQK_LAUNCHED();
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Fused inverted bottleneck: 1x1 expand -> depthwise (stride 1) -> 1x1
+// project [-> residual add with the block input], one 16-wave workgroup per
+// image, every intermediate in LDS. Each phase is the arithmetic of the
+// separate kernels (same records, requantisation and post tables), so the
+// output is identical; only the HBM round trips of the expanded tensors go.
+//   LDS: X [P16][Cin] input | E [P16][Ce] expand out | D [P16][Ce] dw out |
+//        records (expand, dw, project) | dw tap words | add tables | tables
+// P16 = pixels rounded up to 16 (MFMA row tiles; rows past P are never
+// stored). The project output is staged in E (free by then) and written with
+// 16-byte stores.
+// ---------------------------------------------------------------------------
+struct IbArgs {
+    const int8_t *x;
+    int8_t *y;
+    int P, P16, H, W, Cin, Ce, Cout;
+    // expand (1x1): weights [Ce_pad][kpe], records, post table, requant mode
+    const int8_t *we;
+    const int4 *epi_e;
+    const uint8_t *lut_e;
+    int kpe, e_mode, e_yz, e_lo, e_hi;
+    // depthwise: tap words [ky][k][Ce], records, table, mode, zero points
+    const int4 *dww;
+    const int4 *epi_d;
+    const uint8_t *lut_d;
+    int d_mode, d_yz, d_lo, d_hi, d_xz, pt, pl;
+    // project (1x1)
+    const int8_t *wp;
+    const int4 *epi_p;
+    const uint8_t *lut_p;
+    int kpp, p_mode, p_yz, p_lo, p_hi;
+    // residual add (code 18): tables [2][256], operand order, requant
+    int has_add, add_x_first;
+    const int *add_tab;
+    int a_m, a_s, a_yz, a_lo, a_hi;
+    // LDS offsets (bytes)
+    int o_e, o_d, o_re, o_rd, o_rp, o_tw, o_at, o_lut;
+    int cq_magic;              // ceil(2^24 / (Ce / 4))
+    int w_magic;               // ceil(2^16 / W)
+};
+
+__device__ __forceinline__ int ib_requant(int acc, const Epi &e, int mode, int yz, int lo, int hi)
+{
+    switch (mode) {
+    case 0: return conv_requant<false, false>(acc, e, yz, lo, hi);
+    case 1: return conv_requant<true, false>(acc, e, yz, lo, hi);
+    case 2: return conv_requant<false, true>(acc, e, yz, lo, hi);
+    default: return conv_requant<true, true>(acc, e, yz, lo, hi);
+    }
+}
+
+__device__ __forceinline__ Epi ib_epi(const int8_t *smem, int off, int c)
+{
+    return load_epi((const int4 *)(smem + off), c);
+}
+
+// One 1x1 GEMM phase: A rows from LDS (row stride lda bytes, K = k_real
+// valid bytes, kpad columns), B = [n_pad][kpad] weights in HBM. Work items
+// are (row tile, group of NTG column tiles), spread over the 16 waves. The
+// requantised tile goes through `sink(row, col4, word)` as words of four
+// channels of one row.
+template <int NTG, typename Sink>
+__device__ __forceinline__ void ib_gemm(const int8_t *smem, const int8_t *A, int lda, int k_real, int kpad,
+                                        const int8_t *Bw, int ntiles, int mtiles, int epi_off, int mode, int yz, int lo,
+                                        int hi, const int8_t *lut, Sink sink)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int ngroups = (ntiles + NTG - 1) / NTG;
+    const int steps = kpad >> 6;
+    for (int item = wave; item < mtiles * ngroups; item += 16) {
+        const int mt = item / ngroups, ng = item - mt * ngroups;
+        const int nt0 = ng * NTG;
+        v4i acc[NTG];
+#pragma unroll
+        for (int j = 0; j < NTG; j++) acc[j] = (v4i){0, 0, 0, 0};
+        const int8_t *arow = A + (mt * 16 + lr) * lda + lg * 16;
+        for (int st = 0; st < steps; st++) {
+            const int k0 = st * 64 + lg * 16;
+            const v4i a = k0 < k_real ? *(const v4i *)(arow + st * 64) : (v4i){0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < NTG; j++) {
+                if (nt0 + j < ntiles) {
+                    const v4i b = *(const v4i *)(Bw + (long)((nt0 + j) * 16 + lr) * kpad + k0);
+                    acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[j], 0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NTG; j++) {
+            if (nt0 + j >= ntiles) break;
+            const int col = (nt0 + j) * 16 + lr;
+            const Epi e = ib_epi(smem, epi_off, col);
+            int v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[i] = ib_requant(acc[j][i], e, mode, yz, lo, hi);
+                if (lut) v[i] = (int)(signed char)lut[v[i] + 128];
+            }
+            const int word = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
+            sink(mt * 16 + lg * 4 + (lane & 3), (nt0 + j) * 16 + (lr & ~3), word);
+        }
+    }
+}
+
+template <int KS>
+__global__ __launch_bounds__(1024) void k_ib(IbArgs a)
+{
+    constexpr int NWK = KS > 4 ? 2 : 1;
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    int8_t *X = smem, *E = smem + a.o_e, *D = smem + a.o_d;
+    const int tid = threadIdx.x;
+    const long n = blockIdx.x;
+    const int8_t *xin = a.x + n * a.P * a.Cin;
+
+    // Phase 0: image, records, tap words, tables into LDS.
+    for (int i = tid; i < (a.P * a.Cin) >> 4; i += 1024) ((v4i *)X)[i] = ((const v4i *)xin)[i];
+    for (int i = tid; i < 2 * a.Ce; i += 1024) {
+        ((int4 *)(smem + a.o_re))[i] = a.epi_e[i];
+        ((int4 *)(smem + a.o_rd))[i] = a.epi_d[i];
+    }
+    for (int i = tid; i < 2 * a.Cout; i += 1024) ((int4 *)(smem + a.o_rp))[i] = a.epi_p[i];
+    for (int i = tid; i < KS * NWK * a.Ce / 4; i += 1024) ((int4 *)(smem + a.o_tw))[i] = a.dww[i];
+    if (a.has_add) for (int i = tid; i < 512; i += 1024) ((int *)(smem + a.o_at))[i] = a.add_tab[i];
+    int8_t *lut_s = smem + a.o_lut;
+    if (tid < 64) {
+        if (a.lut_e) ((int *)lut_s)[tid] = ((const int *)a.lut_e)[tid];
+        if (a.lut_d) ((int *)(lut_s + 256))[tid] = ((const int *)a.lut_d)[tid];
+        if (a.lut_p) ((int *)(lut_s + 512))[tid] = ((const int *)a.lut_p)[tid];
+    }
+    __syncthreads();
+
+    // Phase 1: expand, E = requant(X * We).
+    const int mtiles = a.P16 >> 4;
+    ib_gemm<4>(smem, X, a.Cin, a.Cin, a.kpe, a.we, a.Ce >> 4, mtiles, a.o_re, a.e_mode, a.e_yz, a.e_lo, a.e_hi,
+               a.lut_e ? lut_s : nullptr,
+               [&](int row, int col, int word) { *(int *)(E + row * a.Ce + col) = word; });
+    __syncthreads();
+
+    // Phase 2: depthwise on E, four channels of one pixel per item; each
+    // kernel row's taps are windows of four adjacent columns (4x4 byte
+    // transpose of the column words), dotted with the row's tap words.
+    {
+        const int cq_n = a.Ce >> 2;
+        const int xzw = (a.d_xz & 0xff) * 0x01010101;
+        const int4 *tw = (const int4 *)(smem + a.o_tw);
+        for (int item = tid; item < a.P * cq_n; item += 1024) {
+            const int p = (int)(((unsigned long long)item * (unsigned)a.cq_magic) >> 24);
+            const int cq = item - p * cq_n;
+            const int y = (p * a.w_magic) >> 16, x = p - y * a.W;
+            int acc[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int ky = 0; ky < KS; ky++) {
+                const int iy = y + ky - a.pt;
+                const bool rowin = (unsigned)iy < (unsigned)a.H;
+#pragma unroll
+                for (int k = 0; k < NWK; k++) {
+                    int cw[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int ix = x - a.pl + 4 * k + j;
+                        cw[j] = rowin && (unsigned)ix < (unsigned)a.W ? *(const int *)(E + (iy * a.W + ix) * a.Ce + 4 * cq)
+                                                                       : xzw;
+                    }
+                    int w0, w1, w2, w3;
+                    transpose4x4(cw[0], cw[1], cw[2], cw[3], w0, w1, w2, w3);
+                    const int4 t = tw[(ky * NWK + k) * cq_n + cq];
+                    acc[0] = __builtin_amdgcn_sdot4(w0, t.x, acc[0], false);
+                    acc[1] = __builtin_amdgcn_sdot4(w1, t.y, acc[1], false);
+                    acc[2] = __builtin_amdgcn_sdot4(w2, t.z, acc[2], false);
+                    acc[3] = __builtin_amdgcn_sdot4(w3, t.w, acc[3], false);
+                }
+            }
+            int v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const Epi e = ib_epi(smem, a.o_rd, 4 * cq + i);
+                v[i] = ib_requant(acc[i], e, a.d_mode, a.d_yz, a.d_lo, a.d_hi);
+                if (a.lut_d) v[i] = lut_s[256 + v[i] + 128];
+            }
+            *(int *)(D + p * a.Ce + 4 * cq) = pack4(v[0], v[1], v[2], v[3]);
+        }
+    }
+    __syncthreads();
+
+    // Phase 3: project (+ residual add), staged in E.
+    const int *at = (const int *)(smem + a.o_at);
+    ib_gemm<2>(smem, D, a.Ce, a.Ce, a.kpp, a.wp, a.Cout >> 4, mtiles, a.o_rp, a.p_mode, a.p_yz, a.p_lo, a.p_hi,
+               a.lut_p ? lut_s + 512 : nullptr, [&](int row, int col, int word) {
+                   if (row >= a.P) return;
+                   if (a.has_add) {
+                       const int xr = *(const int *)(X + row * a.Cin + col);
+                       int z[4];
+#pragma unroll
+                       for (int i = 0; i < 4; i++) {
+                           const int yv = sbyte(word, i), xv = sbyte(xr, i);
+                           const int av = a.add_x_first ? xv : yv, bv = a.add_x_first ? yv : xv;
+                           const int sum = at[av + 128] + at[256 + bv + 128];
+                           z[i] = min(max(uq_scale(sum, a.a_m, a.a_s) + a.a_yz, a.a_lo), a.a_hi);
+                       }
+                       word = pack4(z[0], z[1], z[2], z[3]);
+                   }
+                   *(int *)(E + row * a.Cout + col) = word;
+               });
+    __syncthreads();
+    int8_t *yout = a.y + n * a.P * a.Cout;
+    for (int i = tid; i < (a.P * a.Cout) >> 4; i += 1024) ((v4i *)yout)[i] = ((const v4i *)E)[i];
+}
+
+extern "C" size_t uqk_ib_lds(int P, int Cin, int Ce, int Cout, int ks, size_t *offsets)
+{
+    const int P16 = (P + 15) & ~15;
+    const int nwk = ks > 4 ? 2 : 1;
+    size_t o = 0, off[9];
+    off[0] = o; o += (size_t)P16 * Cin;                    // X
+    o = (o + 15) & ~(size_t)15; off[1] = o; o += (size_t)P16 * Ce;   // E (also the staged output)
+    o = (o + 15) & ~(size_t)15; off[2] = o; o += (size_t)P16 * Ce;   // D
+    o = (o + 15) & ~(size_t)15; off[3] = o; o += (size_t)Ce * 32;    // expand records
+    off[4] = o; o += (size_t)Ce * 32;                      // dw records
+    off[5] = o; o += (size_t)Cout * 32;                    // project records
+    off[6] = o; o += (size_t)ks * nwk * Ce * 4;            // tap words
+    o = (o + 15) & ~(size_t)15; off[7] = o; o += 512 * 4;  // add tables
+    off[8] = o; o += 3 * 256;                              // post tables
+    if (offsets) for (int i = 0; i < 9; i++) offsets[i] = off[i];
+    if ((size_t)P16 * Cout > (size_t)P16 * Ce) return 0;   // staged output must fit in E
+    return o;
+}
+
+extern "C" int uqk_ib(const UQKIb *f, const void *x, void *y, uint32_t images)
+{
+    if (!images) return 0;
+    IbArgs a;
+    size_t off[9];
+    const size_t lds = uqk_ib_lds(f->P, f->Cin, f->Ce, f->Cout, f->ks, off);
+    if (!lds || lds > 163840) return (int)hipErrorInvalidValue;
+    a.x = (const int8_t *)x; a.y = (int8_t *)y;
+    a.P = f->P; a.P16 = (f->P + 15) & ~15; a.H = f->H; a.W = f->W; a.Cin = f->Cin; a.Ce = f->Ce; a.Cout = f->Cout;
+    a.we = (const int8_t *)f->we; a.epi_e = (const int4 *)f->epi_e; a.lut_e = (const uint8_t *)f->lut_e;
+    a.kpe = f->kpe; a.e_mode = f->e_mode; a.e_yz = f->e_yz; a.e_lo = f->e_lo; a.e_hi = f->e_hi;
+    a.dww = (const int4 *)f->dww; a.epi_d = (const int4 *)f->epi_d; a.lut_d = (const uint8_t *)f->lut_d;
+    a.d_mode = f->d_mode; a.d_yz = f->d_yz; a.d_lo = f->d_lo; a.d_hi = f->d_hi; a.d_xz = f->d_xz; a.pt = f->pt; a.pl = f->pl;
+    a.wp = (const int8_t *)f->wp; a.epi_p = (const int4 *)f->epi_p; a.lut_p = (const uint8_t *)f->lut_p;
+    a.kpp = f->kpp; a.p_mode = f->p_mode; a.p_yz = f->p_yz; a.p_lo = f->p_lo; a.p_hi = f->p_hi;
+    a.has_add = f->has_add; a.add_x_first = f->add_x_first; a.add_tab = (const int *)f->add_tab;
+    a.a_m = f->a_m; a.a_s = f->a_s; a.a_yz = f->a_yz; a.a_lo = f->a_lo; a.a_hi = f->a_hi;
+    a.o_e = (int)off[1]; a.o_d = (int)off[2]; a.o_re = (int)off[3]; a.o_rd = (int)off[4]; a.o_rp = (int)off[5];
+    a.o_tw = (int)off[6]; a.o_at = (int)off[7]; a.o_lut = (int)off[8];
+    a.cq_magic = (int)((16777216u + (unsigned)(f->Ce / 4) - 1) / (unsigned)(f->Ce / 4));
+    a.w_magic = (65536 + f->W - 1) / f->W;
+    // The dynamic-LDS ceiling is raised once per kernel (a host call that
+    // must not sit on every launch).
+    static int ceiling_set[2];
+    const int which = f->ks == 3 ? 0 : 1;
+    if (!ceiling_set[which]) {
+        if (which == 0) UQK_TRY(hipFuncSetAttribute((const void *)k_ib<3>, hipFuncAttributeMaxDynamicSharedMemorySize, 163840));
+        else UQK_TRY(hipFuncSetAttribute((const void *)k_ib<5>, hipFuncAttributeMaxDynamicSharedMemorySize, 163840));
+        ceiling_set[which] = 1;
+    }
+    if (which == 0) hipLaunchKernelGGL(k_ib<3>, dim3(images), dim3(1024), lds, g_stream, a);
+    else hipLaunchKernelGGL(k_ib<5>, dim3(images), dim3(1024), lds, g_stream, a);
     UQK_LAUNCHED();
     return 0;
 }

@@ -48,6 +48,27 @@ enum { UQK_PW = 0, UQK_G16 = 1, UQK_G4 = 2, UQK_G1 = 3, UQK_ROWS16 = 4, UQK_ROWS
  * stride 1 or 2, no dilation). */
 size_t uqk_dw_win_lds(const UQKSpatial *d);
 
+/* Fused inverted bottleneck (1x1 expand -> stride-1 depthwise -> 1x1
+ * project [-> residual add with the block input]), one workgroup per image.
+ * Device tables are the three layers' own prepared tables. */
+typedef struct {
+    int32_t P, H, W, Cin, Ce, Cout, ks, pt, pl;
+    const void *we, *epi_e, *lut_e;
+    int32_t kpe, e_mode, e_yz, e_lo, e_hi;
+    const void *dww, *epi_d, *lut_d;
+    int32_t d_mode, d_yz, d_lo, d_hi, d_xz;
+    const void *wp, *epi_p, *lut_p;
+    int32_t kpp, p_mode, p_yz, p_lo, p_hi;
+    int32_t has_add, add_x_first;
+    const void *add_tab;       /* the add's two 256-entry int32 tables */
+    int32_t a_m, a_s, a_yz, a_lo, a_hi;
+} UQKIb;
+
+/* LDS bytes of the fused block for one image (0 if its staged output would
+ * not fit); offsets[9] receives the region offsets when non-null. */
+size_t uqk_ib_lds(int P, int Cin, int Ce, int Cout, int ks, size_t *offsets);
+int uqk_ib(const UQKIb *f, const void *x, void *y, uint32_t images);
+
 /* Whether a conv layer fits the stem kernel's row staging (input rows a
  * multiple of 16 bytes, staged rows within 48 KiB). */
 int uqk_conv_stem_ok(const UQKSpatial *d);
@@ -83,6 +104,20 @@ int uqk_graph_launch(void *exec);
 void uqk_graph_destroy(void *exec);
 
 int uqk_conv(const UQKSpatial *d, const void *x, void *y, uint32_t batches);
+
+/* A residual add (op 18) applied in a conv's epilogue: y = add(conv(x), res)
+ * (or add(res, conv(x)) when conv_is_a is 0), byte for byte the add op's
+ * arithmetic on the conv's int8 output. res has the conv output's layout. */
+typedef struct {
+    const void *res;
+    const void *tables;        /* the add's two 256-entry int32 tables (operand a, then b) */
+    int32_t m, s, yz, lo, hi;
+    int32_t conv_is_a;
+} UQKAdd;
+
+/* Whether uqk_conv_add takes a layer (the k_conv kernel modes). */
+int uqk_conv_add_ok(const UQKSpatial *d);
+int uqk_conv_add(const UQKSpatial *d, const void *x, void *y, uint32_t batches, const UQKAdd *add);
 int uqk_depthwise(const UQKSpatial *d, const void *x, void *y, uint32_t batches);
 int uqk_pool(const UQKSpatial *d, const void *x, void *y, uint32_t batches);
 int uqk_add(const void *a, const void *b, void *y, uint64_t count, const void *tables,
