@@ -529,7 +529,7 @@ static ConvPlan conv_plan(const Op *o)
     int pointwise = q[0] == 1 && q[1] == 1 && q[2] == 1 && q[3] == 1 && !q[6] && !q[7] && !q[8] && !q[9];
     UQKSpatial st;
     memset(&st, 0, sizeof st);
-    st.iw = (int)G.ts[o->a].d[2]; st.ic = ic; st.kh = q[0]; st.sh = q[2]; st.dh = q[4];
+    st.iw = (int)G.ts[o->a].d[2]; st.ic = ic; st.kh = q[0]; st.sh = q[2]; st.dh = q[4]; st.oc = oc;
     if (ic <= 4 && q[0] * q[1] <= 16 && G.ts[o->a].rank == 4 && uqk_conv_stem_ok(&st)) {
         /* Stem form: every tap one 4-byte word, one 64-byte K step; the
          * channel slice spans the padded OC when that is at most 64. */

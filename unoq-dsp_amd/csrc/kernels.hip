@@ -385,7 +385,7 @@ __device__ __forceinline__ void rows_transpose4(int (&r)[4])
 // go through rows_transpose4, after which row j of the wave holds all 16
 // channels of one pixel of row block rb0 + j: one 16-byte store per lane, no
 // LDS round trip. Only one tile's four channel records and four words are
-// live at a time.
+// live at a time. Needs OC % 16 == 0.
 template <int RB, int NT, bool HI, bool CORR>
 __device__ __forceinline__ void conv_store_direct(const ConvArgs &a, const v4i (&acc)[RB][NT], int n0, int lane,
                                                   long row_base, long row_limit, const int4 *epi_s,
@@ -416,32 +416,8 @@ __device__ __forceinline__ void conv_store_direct(const ConvArgs &a, const v4i (
             }
             rows_transpose4(r);
             const long row = row_base + (rb0 + lg) * 16 + lr;
-            if (row >= row_limit || cb >= a.oc) continue;
-            int8_t *dst = a.y + row * a.oc + cb;
-            if ((a.oc & 15) == 0) {
-                *(v4i *)dst = (v4i){r[0], r[1], r[2], r[3]};
-            } else {
-                const int rem = min(16, a.oc - cb);
-#pragma nounroll
-                for (int b = 0; b < rem; b++) {
-                    const int w = b < 4 ? r[0] : b < 8 ? r[1] : b < 12 ? r[2] : r[3];
-                    dst[b] = (int8_t)(w >> (8 * (b & 3)));
-                }
-            }
+            if (row < row_limit && cb < a.oc) *(v4i *)(a.y + row * a.oc + cb) = (v4i){r[0], r[1], r[2], r[3]};
         }
-    }
-}
-
-template <int RB, int NT>
-__device__ __forceinline__ void conv_epilogue_direct(const ConvArgs &a, const v4i (&acc)[RB][NT], int n0, int lane,
-                                                     long row_base, long row_limit, const int4 *epi_s,
-                                                     const int8_t *lut_s)
-{
-    switch (a.emode) {
-    case 0: conv_store_direct<RB, NT, false, false>(a, acc, n0, lane, row_base, row_limit, epi_s, lut_s); break;
-    case 1: conv_store_direct<RB, NT, true, false>(a, acc, n0, lane, row_base, row_limit, epi_s, lut_s); break;
-    case 2: conv_store_direct<RB, NT, false, true>(a, acc, n0, lane, row_base, row_limit, epi_s, lut_s); break;
-    default: conv_store_direct<RB, NT, true, true>(a, acc, n0, lane, row_base, row_limit, epi_s, lut_s); break;
     }
 }
 
@@ -457,6 +433,21 @@ __device__ __forceinline__ void conv_epilogue(const ConvArgs &a, const v4i (&acc
     case 2: conv_store<RB, NT, false, true>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s, add_s, rw); break;
     default: conv_store<RB, NT, true, true>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s, add_s, rw); break;
     }
+}
+
+// The same with the requantisation variant fixed at compile time (EMODE =
+// HI | CORR << 1), or chosen at run time when EMODE < 0. One variant per
+// kernel keeps its register allocation to what that variant needs.
+template <int RB, int NT, int EMODE>
+__device__ __forceinline__ void conv_epilogue_em(const ConvArgs &a, const v4i (&acc)[RB][NT], int8_t *stage, int n0,
+                                                 int lane, long row_base, long row_limit, const int4 *epi_s,
+                                                 const int8_t *lut_s, const int *add_s, const int (&rw)[RB][NT])
+{
+    if constexpr (EMODE < 0)
+        conv_epilogue<RB, NT>(a, acc, stage, n0, lane, row_base, row_limit, epi_s, lut_s, add_s, rw);
+    else
+        conv_store<RB, NT, (EMODE & 1) != 0, (EMODE & 2) != 0>(a, acc, stage, n0, lane, row_base, row_limit, epi_s,
+                                                               lut_s, add_s, rw);
 }
 
 // Without a fused add.
@@ -526,7 +517,7 @@ __host__ __device__ inline size_t conv_lds(int kpad, int rb, int nt)
     return w > st ? w : st;
 }
 
-template <int RB, int NT, int MODE>
+template <int RB, int NT, int MODE, int EMODE>
 __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
 {
     constexpr int R = RB * 16;
@@ -639,8 +630,8 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
         add_s[256 + threadIdx.x] = a.add_tab[256 + threadIdx.x];
     }
     __syncthreads();
-    conv_epilogue<RB, NT>(a, acc, smem + wave * R * STRIDE, n0, lane, row0, a.M, epi_s, lut_s,
-                          a.res ? add_s : nullptr, rw);
+    conv_epilogue_em<RB, NT, EMODE>(a, acc, smem + wave * R * STRIDE, n0, lane, row0, a.M, epi_s, lut_s,
+                                    a.res ? add_s : nullptr, rw);
 }
 
 // Spatial conv with the block's input rows staged in LDS. A block covers BM =
@@ -650,7 +641,7 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
 // WORDS: IC % 16 != 0. Each staged pixel holds icp = IC rounded up to four
 // bytes (the extra channels are zero, and so are their weights), K counts
 // icp-wide taps, and an A slice is four aligned 4-byte LDS reads.
-template <int RB, int NT, bool WORDS>
+template <int RB, int NT, bool WORDS, int EMODE>
 __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
 {
     constexpr int R = RB * 16;
@@ -813,7 +804,9 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
         }
     }
     const long img0 = n * a.ohw;
-    conv_epilogue<RB, NT>(a, acc, stage, n0, lane, img0 + p0 + wave * R, img0 + pend, epi_s, lut_s);
+    const int rw[RB][NT] = {};
+    conv_epilogue_em<RB, NT, EMODE>(a, acc, stage, n0, lane, img0 + p0 + wave * R, img0 + pend, epi_s, lut_s,
+                                    nullptr, rw);
 }
 
 // Stem convolution: at most four input channels and 16 taps (kh * kw), so
@@ -829,10 +822,11 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
 // weights, and padding positions use the zero-point word. The channels are
 // the MFMA's rows, so the requantised bytes leave straight from registers
 // (conv_store_direct).
-template <int RB, int NT>
+template <int RB, int NT, int EMODE>
 __global__ __launch_bounds__(256) void k_conv_stem(ConvArgs a)
 {
     constexpr int R = RB * 16;
+    constexpr bool HI = EMODE & 1, CORR = EMODE & 2;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     __shared__ __attribute__((aligned(4))) int8_t lut_s[256];
     __shared__ int4 epi_s[2 * NT * 16];
@@ -848,8 +842,9 @@ __global__ __launch_bounds__(256) void k_conv_stem(ConvArgs a)
     const int n0 = blockIdx.y * NT * 16;
     const int xzw = (a.xz & 0xff) * 0x01010101;
     const int rowbytes = a.iw * a.ic;                  // a multiple of 16 (host checked)
+    const int gend = a.ih * rowbytes;                  // image bytes (< 2^31, host checked)
     const int iy_base = oy0 * a.sh - a.pt;             // input row of staged row 0
-    const int8_t *xim = a.x + (long)n * a.ih * rowbytes;
+    const int8_t *xim = a.x + (long)n * gend;
 
     const int8_t *wrow = a.w + (long)(n0 + lr) * a.kpad + lg * 16;
     v4i B[NT];
@@ -861,19 +856,18 @@ __global__ __launch_bounds__(256) void k_conv_stem(ConvArgs a)
     // image are skipped (never read). Four loads per thread are issued before
     // the first LDS write.
     {
-        const int total = a.stem_rows * (rowbytes >> 4);
-        const long g0 = (long)iy_base * rowbytes, gend = (long)a.ih * rowbytes;
+        const int total = a.stem_rows * (rowbytes >> 4), g0 = iy_base * rowbytes;
         for (int c0 = threadIdx.x; c0 < total; c0 += 4 * 256) {
             v4i v[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const long g = g0 + (long)(c0 + j * 256) * 16;
-                if (c0 + j * 256 < total && g >= 0 && g < gend) v[j] = *(const v4i *)(xim + g);
+                const int c = c0 + j * 256, g = g0 + c * 16;
+                if (c < total && g >= 0 && g < gend) v[j] = *(const v4i *)(xim + g);
             }
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const long g = g0 + (long)(c0 + j * 256) * 16;
-                if (c0 + j * 256 < total && g >= 0 && g < gend) ((v4i *)smem)[c0 + j * 256] = v[j];
+                const int c = c0 + j * 256, g = g0 + c * 16;
+                if (c < total && g >= 0 && g < gend) ((v4i *)smem)[c] = v[j];
             }
         }
     }
@@ -923,32 +917,40 @@ __global__ __launch_bounds__(256) void k_conv_stem(ConvArgs a)
     // Output pixels of this wave: its output row, ox0 .. min(ox0 + R, ow).
     const long rbase = ((long)n * a.oh + oy) * a.ow + ox0;
     const long rlimit = row_ok ? ((long)n * a.oh + oy) * a.ow + a.ow : rbase;
-    conv_epilogue_direct<RB, NT>(a, acc, n0, lane, rbase, rlimit, epi_s, lut_s);
+    conv_store_direct<RB, NT, HI, CORR>(a, acc, n0, lane, rbase, rlimit, epi_s, lut_s);
 }
 
-// Dynamic LDS of k_conv_stem (staged input rows plus one word of slack for
+// Dynamic LDS of k_conv_stem (staged input rows plus 16 bytes of slack for
 // the second word of the last tap), 0 when the layer does not fit it: the
-// rows must be a multiple of 16 bytes and the staged rows at most 48 KiB.
+// rows must be a multiple of 16 bytes, the staged rows at most 48 KiB, and OC
+// a multiple of 16 (whole 16-byte stores).
 static size_t stem_lds(const UQKSpatial *d)
 {
     const int rowbytes = d->iw * d->ic;
     const int rows = 3 * d->sh + (d->kh - 1) * d->dh + 1;
     const size_t bytes = (size_t)rows * rowbytes + 16;
-    return rowbytes % 16 == 0 && bytes <= 49152 ? bytes : 0;
+    return rowbytes % 16 == 0 && d->oc % 16 == 0 && bytes <= 49152 ? bytes : 0;
 }
 
 extern "C" int uqk_conv_stem_ok(const UQKSpatial *d) { return stem_lds(d) > 0; }
 
 template <int RB, int NT>
-static void launch_conv_mode(int mode, const ConvArgs &a, dim3 grid, size_t lds)
+static void launch_conv_mode(int mode, const ConvArgs &a, dim3 grid, size_t)
 {
+    const size_t lds = conv_lds(a.kpad, RB, NT);
     switch (mode) {
-    case UQK_PW: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW>), grid, dim3(256), conv_lds(a.kpad, RB, NT), g_stream, a); break;
-    case UQK_G16: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G16>), grid, dim3(256), conv_lds(a.kpad, RB, NT), g_stream, a); break;
-    case UQK_G4: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G4>), grid, dim3(256), conv_lds(a.kpad, RB, NT), g_stream, a); break;
-    case UQK_G1: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G1>), grid, dim3(256), conv_lds(a.kpad, RB, NT), g_stream, a); break;
-    case UQK_ROWS16: hipLaunchKernelGGL((k_conv_rows<RB, NT, false>), grid, dim3(256), lds, g_stream, a); break;
-    default: hipLaunchKernelGGL((k_conv_rows<RB, NT, true>), grid, dim3(256), lds, g_stream, a); break;
+    case UQK_PW:
+        // The common case: one kernel per requantisation variant.
+        switch (a.emode) {
+        case 0: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 0>), grid, dim3(256), lds, g_stream, a); break;
+        case 1: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 1>), grid, dim3(256), lds, g_stream, a); break;
+        case 2: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 2>), grid, dim3(256), lds, g_stream, a); break;
+        default: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 3>), grid, dim3(256), lds, g_stream, a); break;
+        }
+        break;
+    case UQK_G16: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G16, -1>), grid, dim3(256), lds, g_stream, a); break;
+    case UQK_G4: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G4, -1>), grid, dim3(256), lds, g_stream, a); break;
+    default: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G1, -1>), grid, dim3(256), lds, g_stream, a); break;
     }
 }
 
@@ -966,10 +968,19 @@ static void launch_conv_nt(int nt, int mode, const ConvArgs &a, dim3 grid, size_
 template <int RB>
 static void launch_rows_nt(int nt, int mode, const ConvArgs &a, dim3 grid, size_t lds)
 {
+#define UQK_ROWS_EM(NT, W)                                                                                      \
+    do {                                                                                                        \
+        switch (a.emode) {                                                                                      \
+        case 0: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 0>), grid, dim3(256), lds, g_stream, a); break;      \
+        case 1: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 1>), grid, dim3(256), lds, g_stream, a); break;      \
+        case 2: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 2>), grid, dim3(256), lds, g_stream, a); break;      \
+        default: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 3>), grid, dim3(256), lds, g_stream, a); break;     \
+        }                                                                                                       \
+    } while (0)
 #define UQK_ROWS_LAUNCH(NT)                                                                                     \
     do {                                                                                                        \
-        if (mode == UQK_ROWS16) hipLaunchKernelGGL((k_conv_rows<RB, NT, false>), grid, dim3(256), lds, g_stream, a); \
-        else hipLaunchKernelGGL((k_conv_rows<RB, NT, true>), grid, dim3(256), lds, g_stream, a);              \
+        if (mode == UQK_ROWS16) UQK_ROWS_EM(NT, false);                                                         \
+        else UQK_ROWS_EM(NT, true);                                                                             \
     } while (0)
     switch (nt) {
     case 2: UQK_ROWS_LAUNCH(2); break;
@@ -978,6 +989,7 @@ static void launch_rows_nt(int nt, int mode, const ConvArgs &a, dim3 grid, size_
     default: UQK_ROWS_LAUNCH(8); break;
     }
 #undef UQK_ROWS_LAUNCH
+#undef UQK_ROWS_EM
 }
 
 // Bytes of dynamic LDS the row-staged kernel needs for one layer.
@@ -1037,31 +1049,34 @@ static int conv_launch(const UQKSpatial *d, const void *x, void *y, uint32_t bat
     if (a.M <= 0) return 0;
     const int nchunks = d->oc_pad / (16 * d->nt);
     if (d->mode == UQK_STEM) {
-        // One row segment per wave, four rows per block; the channel
-        // slice covers up to 64 channels (NT = oc_pad / 16 when that is 1, 2
-        // or 4).
+        // A block is four output rows x one 64-pixel segment per wave (four
+        // row blocks: wider segments cost waves per SIMD, which this
+        // latency-bound kernel needs more); the channel slice covers up to 64
+        // channels (NT = oc_pad / 16 when that is 1, 2 or 4).
         const int nt = d->oc_pad == 16 ? 1 : d->oc_pad == 32 ? 2 : 4;
         a.images = (int)batches;
-        // 128-pixel segments (eight row blocks per wave) on wide rows: more
-        // loads in flight per wave.
-        const int rbk = d->ow > 64 ? 8 : 4;
-        a.segs = (d->ow + 16 * rbk - 1) / (16 * rbk);
+        a.segs = (d->ow + 63) / 64;
         a.row_groups = (d->oh + 3) / 4;
         a.kw_magic = (65536 + d->kw - 1) / d->kw;
         a.stem_rows = 3 * d->sh + (d->kh - 1) * d->dh + 1;
         const size_t lds = stem_lds(d);
-        const unsigned long long blocks = (unsigned long long)batches * a.row_groups * a.segs;
-        if (!lds || blocks > 0x7fffffffULL) return (int)hipErrorInvalidValue;
-        dim3 grid((unsigned)blocks, (unsigned)(d->oc_pad / (16 * nt)));
-#define UQK_STEM_NT(RBK)                                                                                  \
-    do {                                                                                                  \
-        if (nt == 1) hipLaunchKernelGGL((k_conv_stem<RBK, 1>), grid, dim3(256), lds, g_stream, a);       \
-        else if (nt == 2) hipLaunchKernelGGL((k_conv_stem<RBK, 2>), grid, dim3(256), lds, g_stream, a);  \
-        else hipLaunchKernelGGL((k_conv_stem<RBK, 4>), grid, dim3(256), lds, g_stream, a);               \
+        const unsigned long long items = (unsigned long long)batches * a.row_groups * a.segs;
+        if (!lds || items > 0x7fffffffULL || (unsigned long long)d->ih * d->iw * d->ic > 0x7fffffffULL)
+            return (int)hipErrorInvalidValue;
+        dim3 grid((unsigned)items, (unsigned)(d->oc_pad / (16 * nt)));
+#define UQK_STEM_EM(NT)                                                                                    \
+    do {                                                                                                   \
+        switch (a.emode) {                                                                                 \
+        case 0: hipLaunchKernelGGL((k_conv_stem<4, NT, 0>), grid, dim3(256), lds, g_stream, a); break;     \
+        case 1: hipLaunchKernelGGL((k_conv_stem<4, NT, 1>), grid, dim3(256), lds, g_stream, a); break;     \
+        case 2: hipLaunchKernelGGL((k_conv_stem<4, NT, 2>), grid, dim3(256), lds, g_stream, a); break;     \
+        default: hipLaunchKernelGGL((k_conv_stem<4, NT, 3>), grid, dim3(256), lds, g_stream, a); break;    \
+        }                                                                                                  \
     } while (0)
-        if (rbk == 8) UQK_STEM_NT(8);
-        else UQK_STEM_NT(4);
-#undef UQK_STEM_NT
+        if (nt == 1) UQK_STEM_EM(1);
+        else if (nt == 2) UQK_STEM_EM(2);
+        else UQK_STEM_EM(4);
+#undef UQK_STEM_EM
         UQK_LAUNCHED();
         return 0;
     }

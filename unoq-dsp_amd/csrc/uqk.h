@@ -69,8 +69,8 @@ typedef struct {
 size_t uqk_ib_lds(int P, int Cin, int Ce, int Cout, int ks, size_t *offsets);
 int uqk_ib(const UQKIb *f, const void *x, void *y, uint32_t images);
 
-/* Whether a conv layer fits the stem kernel's row staging (input rows a
- * multiple of 16 bytes, staged rows within 48 KiB). */
+/* Whether a conv layer fits the stem kernel (input rows a multiple of 16
+ * bytes, its staged rows within 48 KiB, OC % 16 == 0). */
 int uqk_conv_stem_ok(const UQKSpatial *d);
 
 /* Dynamic LDS bytes k_conv_rows needs for a layer at rb row blocks per wave. */
