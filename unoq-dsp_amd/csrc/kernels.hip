@@ -115,12 +115,26 @@ struct ConvArgs {
     int ih, iw, ic, icp, oh, ow, oc, kh, sh, sw, dh, pt, pl, xz, yz, lo, hi, K, kpad, ohw, corr, emode;
     int kw, dw, taps;
     int images, segs, row_groups, kw_magic, stem_rows;   // stem grid, tap decomposition, staged rows
-    int tiles, cols, rows_max;
+    int tiles, cols, rows_max, tile_px;
+    unsigned m_row, m_px;      // k_conv_rows staging: udiv_magic of items per staged row, per pixel
     // Fused residual add (k_conv only; res == nullptr when there is none).
     const int8_t *res;
     const int *add_tab;
     int add_m, add_s, add_yz, add_lo, add_hi, add_conv_a;
 };
+
+// x / d without a division: ceil(2^32 / d) as a multiply-high, exact when
+// x * d < 2^32 (the rounding error of the magic is below d); d == 1 passes
+// x through. The magic comes from udiv_magic on the host.
+__device__ __forceinline__ unsigned udiv(unsigned x, unsigned d, unsigned magic)
+{
+    return d == 1 ? x : __umulhi(x, magic);
+}
+
+static inline unsigned udiv_magic(unsigned d)
+{
+    return d <= 1 ? 0u : (unsigned)((0x100000000ULL + d - 1) / d);
+}
 
 template <int MODE>
 __device__ __forceinline__ v4i gather16(const ConvArgs &a, const int8_t *base, int iy0, int ix0, bool valid, int kg, int xzw)
@@ -655,7 +669,7 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
     const int tile = blockIdx.x % a.tiles;
     const long n = blockIdx.x / a.tiles;
     const int n0 = blockIdx.y * NT * 16;
-    const int p0 = tile * BM, pend = min(p0 + BM, a.ohw);
+    const int p0 = tile * a.tile_px, pend = min(p0 + a.tile_px, a.ohw);   // tile_px <= BM
     const int oy_a = p0 / a.ow, oy_b = (pend - 1) / a.ow;
     const int rows = (oy_b - oy_a) * a.sh + (a.kh - 1) * a.dh + 1;
     const int rowbytes = a.cols * a.icp;
@@ -671,16 +685,18 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
     // Staging: each thread issues STAGE_U loads before its first LDS write,
     // so a block waits for about one HBM latency, not one per staged row.
     constexpr int STAGE_U = 4;
+    // Staged item q -> (row, column, channel offset) by multiply-high (q,
+    // the row width and the pixel width are all below 2^16).
     if (!WORDS) {
         const int xzw = (a.xz & 0xff) * 0x01010101;
-        const int cpr = rowbytes >> 4, total = rows * cpr;
+        const int cpr = rowbytes >> 4, total = rows * cpr, ic16 = a.ic >> 4;
         for (int q0 = threadIdx.x; q0 < total; q0 += STAGE_U * 256) {
             v4i v[STAGE_U];
 #pragma unroll
             for (int j = 0; j < STAGE_U; j++) {
                 const int q = q0 + j * 256;
-                const int r = q / cpr, b = (q - r * cpr) << 4;
-                const int col = b / a.ic, c = b - col * a.ic;
+                const int r = (int)udiv((unsigned)q, (unsigned)cpr, a.m_row), b16 = q - r * cpr;
+                const int col = (int)udiv((unsigned)b16, (unsigned)ic16, a.m_px), c = (b16 - col * ic16) << 4;
                 const int iy = iy_lo + r, ix = col - a.pl;
                 v[j] = (v4i){xzw, xzw, xzw, xzw};
                 if (q < total && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw)
@@ -699,8 +715,8 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
 #pragma unroll
             for (int j = 0; j < STAGE_U; j++) {
                 const int q = q0 + j * 256;
-                const int r = q / wpr, wi = q - r * wpr;
-                const int col = wpp == 1 ? wi : wi / wpp, cw = wi - col * wpp;
+                const int r = (int)udiv((unsigned)q, (unsigned)wpr, a.m_row), wi = q - r * wpr;
+                const int col = (int)udiv((unsigned)wi, (unsigned)wpp, a.m_px), cw = wi - col * wpp;
                 const int iy = iy_lo + r, ix = col - a.pl;
                 const bool in = q < total && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
                 const int8_t *src = xim + (in ? ((long)iy * a.iw + ix) * a.ic : 0) + cw * 4;
@@ -736,7 +752,7 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
     // LDS): steps s + 1 .. s + P - 1 are in flight while step s multiplies.
     // (Staging them in LDS as k_conv does costs these blocks occupancy: the
     // pixel tile already holds most of the block's LDS.)
-    constexpr int P = 96 / (NT * 4) >= 8 ? 8 : 96 / (NT * 4) >= 4 ? 4 : 2;
+    constexpr int P = 48 / (NT * 4) >= 8 ? 8 : 48 / (NT * 4) >= 4 ? 4 : 2;
     const int8_t *wrow = a.w + (long)(n0 + lr) * a.kpad + lg * 16;
     const int steps = a.kpad >> 6;
     v4i B[P][NT];
@@ -993,11 +1009,26 @@ static void launch_rows_nt(int nt, int mode, const ConvArgs &a, dim3 grid, size_
 }
 
 // Bytes of dynamic LDS the row-staged kernel needs for one layer.
+// Output pixels per k_conv_rows tile: whole output rows when at least one
+// fits the block's 64*rb pixels (then a tile's input rows overlap its
+// neighbours' only by the kernel's halo), else 64*rb consecutive pixels.
+// Sets *span to the most output rows one tile touches.
+static int rows_tile(const UQKSpatial *d, int rb, int *span)
+{
+    const int bm = 4 * 16 * rb, rpt = bm / d->ow;
+    if (rpt >= 1) {
+        *span = rpt;
+        return rpt * d->ow;
+    }
+    *span = (bm + d->ow - 2) / d->ow + 1;   // bm consecutive pixels from any column
+    return bm;
+}
+
 extern "C" size_t uqk_conv_rows_lds(const UQKSpatial *d, int rb)
 {
-    const int bm = 4 * 16 * rb;
-    const int span = (bm + d->ow - 2) / d->ow;
-    const int rows_max = span * d->sh + (d->kh - 1) * d->dh + 1;
+    int span;
+    rows_tile(d, rb, &span);
+    const int rows_max = (span - 1) * d->sh + (d->kh - 1) * d->dh + 1;
     const int cols = (d->ow - 1) * d->sw + (d->kw - 1) * d->dw + 1;
     const int ndelta = d->mode == UQK_ROWS16 ? d->K / 16 : d->K / 4;
     const int icp = d->mode == UQK_ROWS16 ? d->ic : (d->ic + 3) & ~3;
@@ -1082,9 +1113,20 @@ static int conv_launch(const UQKSpatial *d, const void *x, void *y, uint32_t bat
     }
     if (d->mode == UQK_ROWS16 || d->mode == UQK_ROWS4) {
         // Larger tiles stage fewer redundant input rows per output row.
-        const int rb = d->mode == UQK_ROWS4 && d->nt <= 4 && uqk_conv_rows_lds(d, 4) <= 65536 ? 4 : 2, bm = 4 * 16 * rb;
-        a.tiles = (a.ohw + bm - 1) / bm;
-        a.rows_max = ((bm + d->ow - 2) / d->ow) * d->sh + (d->kh - 1) * d->dh + 1;
+        const int rb = d->nt <= 4 && uqk_conv_rows_lds(d, 4) <= 65536 ? 4 : 2;
+        int span;
+        a.tile_px = rows_tile(d, rb, &span);
+        a.tiles = (a.ohw + a.tile_px - 1) / a.tile_px;
+        a.rows_max = (span - 1) * d->sh + (d->kh - 1) * d->dh + 1;
+        {
+            // Staging divisors: items per staged row and per pixel (16-byte
+            // chunks for ROWS16, words for ROWS4).
+            const unsigned per_px = d->mode == UQK_ROWS16 ? (unsigned)d->ic / 16 : (unsigned)((d->ic + 3) & ~3) / 4;
+            const unsigned per_row = (unsigned)a.cols * per_px;
+            if ((unsigned long long)a.rows_max * per_row >= 65536ULL) return (int)hipErrorInvalidValue;
+            a.m_row = udiv_magic(per_row);
+            a.m_px = udiv_magic(per_px);
+        }
         dim3 grid((unsigned)((long)batches * a.tiles), (unsigned)nchunks);
         if (rb == 4) launch_rows_nt<4>(d->nt, d->mode, a, grid, uqk_conv_rows_lds(d, rb));
         else launch_rows_nt<2>(d->nt, d->mode, a, grid, uqk_conv_rows_lds(d, rb));
