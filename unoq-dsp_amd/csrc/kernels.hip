@@ -1611,6 +1611,183 @@ static int launch_dw_win(const UQKSpatial *d, const void *x, void *y, uint32_t b
 }
 
 // ---------------------------------------------------------------------------
+// Depthwise on the matrix cores (KS 3 or 5, stride 1 or 2, C % 16 == 0).
+//
+// One MFMA computes 16 output pixels x 16 channels over four taps: the K
+// dimension is (tap, channel) with 16 channels per tap, the pixel operand of
+// lane (pixel lr, slice lg) is the 16 channel bytes of the input pixel under
+// tap 4m + lg (one 16-byte LDS read, NHWC as staged, no transposes), and the
+// weight operand is block-diagonal: lane (channel lr, slice lg) holds
+// w[tap 4m + lg][channel lr] in byte lr and zeros elsewhere. ceil(KS*KS / 4)
+// MFMAs (7 for 5x5, 3 for 3x3) give the depthwise sums of a 16 x 16 tile;
+// taps past KS*KS carry zero weights. The products and their sum are the
+// signed int8 ones of the dot4 kernel, so the same records requantise them.
+//
+// A block is one image x GB groups of 16 channels (GB = 1, 2 or 4; more for
+// small maps, whose images have few tiles): the padded input window the
+// image's outputs need ((OH-1)*S + KS rows and columns, padding as the zero
+// point) is staged once in LDS, one plane per group, and the 4/GB waves of a
+// group take 16-pixel tiles of the image's flattened output in turn (so 7x7
+// maps waste only the last tile's tail). Blocks are ordered channel groups
+// outer, image inner, so the groups of one image share an XCD (and its L2)
+// when the image count is a multiple of 8.
+// ---------------------------------------------------------------------------
+struct DwMArgs {
+    const int8_t *x;
+    int8_t *y;
+    const int *wdot;           // [ky][wk][C] words of four taps
+    const int4 *epi;
+    const uint8_t *lut;
+    int ih, iw, c, oh, ow, pt, pl, xz, yz, lo, hi;
+    int images, rows_p, cols_p;
+    int lgb, lwg;              // log2 of channel groups per block, of waves per group
+    unsigned m_cols, m_ow;     // udiv_magic(cols_p), udiv_magic(ow)
+};
+
+template <int KS, int S, bool HI, bool CORR>
+__global__ __launch_bounds__(256) void k_dw_mfma(DwMArgs a)
+{
+    constexpr int T = KS * KS, NG = (T + 3) / 4, NWK = KS > 4 ? 2 : 1;
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    __shared__ __attribute__((aligned(4))) int8_t lut_s[256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int gblock = blockIdx.x / a.images, n = blockIdx.x - gblock * a.images;
+    const int gw = wave >> a.lwg, wsub = wave & ((1 << a.lwg) - 1);   // this wave's group, rank in it
+    const int cblk = gblock << (a.lgb + 4), c0 = cblk + gw * 16;
+    const int xzw = (a.xz & 0xff) * 0x01010101;
+    const int plane = a.rows_p * a.cols_p;          // staged pixels per group
+
+    // Stage the padded window: item q = (staged pixel, group) with the group
+    // fastest (one pixel's GB 16-byte chunks are contiguous in HBM); staged
+    // pixel (r, cc) is input (r - pt, cc - pl).
+    {
+        const int8_t *xim = a.x + (long)n * a.ih * a.iw * a.c + cblk;
+        const int total = plane << a.lgb;
+        for (int q0 = threadIdx.x; q0 < total; q0 += 4 * 256) {
+            v4i v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int q = q0 + j * 256, sp = q >> a.lgb, gq = q & ((1 << a.lgb) - 1);
+                const int r = (int)udiv((unsigned)sp, (unsigned)a.cols_p, a.m_cols), cc = sp - r * a.cols_p;
+                const int iy = r - a.pt, ix = cc - a.pl;
+                const bool in = q < total && (unsigned)iy < (unsigned)a.ih && (unsigned)ix < (unsigned)a.iw;
+                v[j] = (v4i){xzw, xzw, xzw, xzw};
+                if (in) v[j] = *(const v4i *)(xim + ((long)iy * a.iw + ix) * a.c + gq * 16);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int q = q0 + j * 256;
+                if (q < total) ((v4i *)smem)[(q & ((1 << a.lgb) - 1)) * plane + (q >> a.lgb)] = v[j];
+            }
+        }
+    }
+    if (a.lut && threadIdx.x < 64) ((int *)lut_s)[threadIdx.x] = ((const int *)a.lut)[threadIdx.x];
+
+    // This lane's weight operands and tap offsets (LDS bytes from a pixel's
+    // window corner); taps past T use offset 0 and zero weights.
+    v4i B[NG];
+    int off[NG];
+#pragma unroll
+    for (int m = 0; m < NG; m++) {
+        const int t = 4 * m + lg;
+        const int ky = t / KS, kx = t - ky * KS;
+        int wb = 0;
+        if (t < T) wb = (a.wdot[(ky * NWK + (kx >> 2)) * a.c + c0 + lr] >> (8 * (kx & 3))) & 0xff;
+        const int word = wb << (8 * (lr & 3)), at = lr >> 2;
+        B[m] = (v4i){at == 0 ? word : 0, at == 1 ? word : 0, at == 2 ? word : 0, at == 3 ? word : 0};
+        off[m] = t < T ? (ky * a.cols_p + kx) * 16 : 0;
+    }
+    const Epi e = load_epi(a.epi, c0 + lr);
+    __syncthreads();
+
+    const int npix = a.oh * a.ow, tiles = (npix + 15) >> 4;
+    int8_t *yim = a.y + (long)n * npix * a.c + c0;
+    const int8_t *pl = smem + (size_t)gw * plane * 16;
+    for (int tile = wsub; tile < tiles; tile += 1 << a.lwg) {
+        // A row: output pixel p (clamped into the map for the tail tile).
+        const int p = min(tile * 16 + lr, npix - 1);
+        const int oy = (int)udiv((unsigned)p, (unsigned)a.ow, a.m_ow), ox = p - oy * a.ow;
+        const int8_t *base = pl + (oy * S * a.cols_p + ox * S) * 16;
+        v4i A[NG];
+#pragma unroll
+        for (int m = 0; m < NG; m++) A[m] = *(const v4i *)(base + off[m]);
+        v4i acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int m = 0; m < NG; m++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m], B[m], acc, 0, 0, 0);
+        // acc[i]: pixel tile*16 + 4*lg + i, channel c0 + lr.
+        int v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[i], e, a.yz, a.lo, a.hi);
+        if (a.lut) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = lut_s[v[i] + 128];
+        }
+        const int word = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
+        const int px = tile * 16 + lg * 4 + (lane & 3);
+        if (px < npix) *(int *)(yim + (long)px * a.c + (lr & ~3)) = word;
+    }
+}
+
+// Geometry of k_dw_mfma; returns its dynamic LDS bytes, 0 if the layer does
+// not suit it (then the dot4 window kernel runs it).
+static size_t dw_mfma_plan(const UQKSpatial *d, DwMArgs *t)
+{
+    const int ks = d->kh, s = d->sh;
+    if (!d->dwwin || d->oc % 16 || d->ic != d->oc || d->kh != d->kw || (ks != 3 && ks != 5) || d->sh != d->sw ||
+        (s != 1 && s != 2) || d->dh != 1 || d->dw != 1)
+        return 0;
+    t->rows_p = (d->oh - 1) * s + ks;
+    t->cols_p = (d->ow - 1) * s + ks;
+    // Groups per block: enough tiles per wave on small maps (a 7x7 image has
+    // four), a whole number of blocks per image, the planes within 40 KiB.
+    const int tiles = (d->oh * d->ow + 15) / 16, groups = d->oc / 16;
+    int lgb = tiles <= 4 ? 2 : tiles <= 8 ? 1 : 0;
+    while (lgb && (groups % (1 << lgb) || ((size_t)t->rows_p * t->cols_p * 16 << lgb) > 40960)) lgb--;
+    t->lgb = lgb;
+    t->lwg = 2 - lgb;
+    const size_t bytes = (size_t)t->rows_p * t->cols_p * 16 << lgb;
+    if (bytes > 40960 || (long)d->oh * d->ow >= 65536) return 0;
+    t->m_cols = udiv_magic((unsigned)t->cols_p);
+    t->m_ow = udiv_magic((unsigned)d->ow);
+    return bytes;
+}
+
+static int launch_dw_mfma(const UQKSpatial *d, const void *x, void *y, uint32_t batches)
+{
+    DwMArgs a;
+    const size_t lds = dw_mfma_plan(d, &a);
+    if (!lds) return -1;
+    a.x = (const int8_t *)x;
+    a.y = (int8_t *)y;
+    a.wdot = (const int *)d->wdot;
+    a.epi = (const int4 *)d->epi;
+    a.lut = (const uint8_t *)d->lut;
+    a.ih = d->ih; a.iw = d->iw; a.c = d->oc; a.oh = d->oh; a.ow = d->ow; a.pt = d->pt; a.pl = d->pl;
+    a.xz = d->xz; a.yz = d->yz; a.lo = d->lo; a.hi = d->hi;
+    a.images = (int)batches;
+    const unsigned long long blocks = (unsigned long long)batches * (d->oc / 16 >> a.lgb);
+    if (blocks > 0x7fffffffULL || batches == 0) return blocks ? -1 : 0;
+    const int mode = (d->hi_shift ? 1 : 0) | (d->corr ? 2 : 0);
+#define UQK_DWM(K, S)                                                                                           \
+    do {                                                                                                        \
+        switch (mode) {                                                                                         \
+        case 0: hipLaunchKernelGGL((k_dw_mfma<K, S, false, false>), dim3((unsigned)blocks), dim3(256), lds, g_stream, a); break; \
+        case 1: hipLaunchKernelGGL((k_dw_mfma<K, S, true, false>), dim3((unsigned)blocks), dim3(256), lds, g_stream, a); break;  \
+        case 2: hipLaunchKernelGGL((k_dw_mfma<K, S, false, true>), dim3((unsigned)blocks), dim3(256), lds, g_stream, a); break;  \
+        default: hipLaunchKernelGGL((k_dw_mfma<K, S, true, true>), dim3((unsigned)blocks), dim3(256), lds, g_stream, a); break;  \
+        }                                                                                                       \
+    } while (0)
+    if (d->kh == 3 && d->sh == 1) UQK_DWM(3, 1);
+    else if (d->kh == 3) UQK_DWM(3, 2);
+    else if (d->sh == 1) UQK_DWM(5, 1);
+    else UQK_DWM(5, 2);
+#undef UQK_DWM
+    UQK_LAUNCHED();
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
 // Fused inverted bottleneck: 1x1 expand -> depthwise (stride 1) -> 1x1
 // project [-> residual add with the block input], one 16-wave workgroup per
 // image, every intermediate in LDS. Each phase is the arithmetic of the
@@ -1957,7 +2134,11 @@ static int launch_window(const UQKSpatial *d, const void *x, void *y, uint32_t b
 extern "C" int uqk_depthwise(const UQKSpatial *d, const void *x, void *y, uint32_t batches)
 {
     if (!batches) return 0;
-    if (d->dwwin) return launch_dw_win(d, x, y, batches) < 0 ? (int)hipErrorInvalidValue : 0;
+    if (d->dwwin) {
+        DwMArgs t;
+        if (dw_mfma_plan(d, &t)) return launch_dw_mfma(d, x, y, batches) < 0 ? (int)hipErrorInvalidValue : 0;
+        return launch_dw_win(d, x, y, batches) < 0 ? (int)hipErrorInvalidValue : 0;
+    }
     const int rc = launch_dw_tile(d, x, y, batches);
     if (rc >= 0) return rc;
     return launch_window(d, x, y, batches, false);
