@@ -356,7 +356,16 @@ __device__ __forceinline__ void conv_store(const ConvArgs &a, const v4i (&acc)[R
     }
     __syncthreads();
     const int ncols = min(BN, a.oc - n0);
-    if ((a.oc & 15) == 0) {
+    if ((a.oc & 15) == 0 && ncols == BN) {
+        // The whole slice: NT 16-byte chunks per row, a compile-time split.
+#pragma unroll
+        for (int c = lane; c < R * NT; c += 64) {
+            const int r = c / NT, cc = c - r * NT;
+            const long row = row_base + r;
+            if (row < row_limit)
+                *(v4i *)(a.y + row * a.oc + n0 + cc * 16) = *(const v4i *)(&stage[r * STRIDE + cc * 16]);
+        }
+    } else if ((a.oc & 15) == 0) {
         const int cpr = ncols >> 4;
         for (int c = lane; c < R * cpr; c += 64) {
             const int r = c / cpr, cc = c - r * cpr;
@@ -1742,7 +1751,7 @@ static size_t dw_mfma_plan(const UQKSpatial *d, DwMArgs *t)
     // Groups per block: enough tiles per wave on small maps (a 7x7 image has
     // four), a whole number of blocks per image, the planes within 40 KiB.
     const int tiles = (d->oh * d->ow + 15) / 16, groups = d->oc / 16;
-    int lgb = tiles <= 4 ? 2 : tiles <= 8 ? 1 : 0;
+    int lgb = tiles <= 4 ? 2 : tiles <= 16 ? 1 : 0;
     while (lgb && (groups % (1 << lgb) || ((size_t)t->rows_p * t->cols_p * 16 << lgb) > 40960)) lgb--;
     t->lgb = lgb;
     t->lwg = 2 - lgb;
