@@ -202,6 +202,16 @@ __device__ __forceinline__ int pack4(int v0, int v1, int v2, int v3)
     return (int)(lo | hi);
 }
 
+// A value copied into a VGPR once and opaque to the compiler from then on, so
+// that it stays there: for the clamp bounds of med3, which otherwise are
+// re-copied from their SGPRs before nearly every use.
+__device__ __forceinline__ int vgpr(int x)
+{
+    int r = x;
+    asm volatile("" : "+v"(r));
+    return r;
+}
+
 // Clamp to [lo, hi] in one v_med3_i32 (the compiler keeps min/max apart).
 __device__ __forceinline__ int med3(int x, int lo, int hi)
 {
@@ -330,6 +340,7 @@ __device__ __forceinline__ void conv_store(const ConvArgs &a, const v4i (&acc)[R
     constexpr int BN = NT * 16;
     constexpr int STRIDE = BN + 16;
     const int lr = lane & 15, lg = lane >> 4;
+    const int vlo = vgpr(a.lo), vhi = vgpr(a.hi);
     const bool words = (a.oc & 3) == 0;
     const bool lut = a.lut != nullptr;
 #pragma unroll
@@ -339,7 +350,7 @@ __device__ __forceinline__ void conv_store(const ConvArgs &a, const v4i (&acc)[R
         for (int rb = 0; rb < RB; rb++) {
             int v[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[rb][nt][i], e, a.yz, a.lo, a.hi);
+            for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[rb][nt][i], e, a.yz, vlo, vhi);
             if (lut) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) v[i] = lut_s[v[i] + 128];
@@ -416,6 +427,7 @@ __device__ __forceinline__ void conv_store_direct(const ConvArgs &a, const v4i (
 {
     static_assert(RB % 4 == 0, "row blocks go through the transpose in fours");
     const int lr = lane & 15, lg = lane >> 4;
+    const int vlo = vgpr(a.lo), vhi = vgpr(a.hi);
     const bool lut = a.lut != nullptr;
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
@@ -430,7 +442,7 @@ __device__ __forceinline__ void conv_store_direct(const ConvArgs &a, const v4i (
             for (int q = 0; q < 4; q++) {
                 int v[4];
 #pragma unroll
-                for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[rb0 + q][nt][i], e[i], a.yz, a.lo, a.hi);
+                for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[rb0 + q][nt][i], e[i], a.yz, vlo, vhi);
                 if (lut) {
 #pragma unroll
                     for (int i = 0; i < 4; i++) v[i] = lut_s[v[i] + 128];
@@ -1521,6 +1533,7 @@ __global__ __launch_bounds__(256) void k_dw_win(DwWinArgs a)
     }
     const int oy = oy0 + tyi;
     int8_t *yrow = a.y + ((n * a.oh + oy) * a.ow) * (long)a.c + cbase;
+    const int vlo = vgpr(a.lo), vhi = vgpr(a.hi);
     Epi e[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -1535,7 +1548,7 @@ __global__ __launch_bounds__(256) void k_dw_win(DwWinArgs a)
         if (ox >= a.ow) break;
         int v[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[t][i], e[i], a.yz, a.lo, a.hi);
+        for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[t][i], e[i], a.yz, vlo, vhi);
         if (a.lut) {
 #pragma unroll
             for (int i = 0; i < 4; i++) v[i] = lut_s[v[i] + 128];
@@ -1708,6 +1721,7 @@ __global__ __launch_bounds__(256) void k_dw_mfma(DwMArgs a)
         off[m] = t < T ? (ky * a.cols_p + kx) * 16 : 0;
     }
     const Epi e = load_epi(a.epi, c0 + lr);
+    const int vlo = vgpr(a.lo), vhi = vgpr(a.hi);
     __syncthreads();
 
     const int npix = a.oh * a.ow, tiles = (npix + 15) >> 4;
@@ -1727,7 +1741,7 @@ __global__ __launch_bounds__(256) void k_dw_mfma(DwMArgs a)
         // acc[i]: pixel tile*16 + 4*lg + i, channel c0 + lr.
         int v[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[i], e, a.yz, a.lo, a.hi);
+        for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[i], e, a.yz, vlo, vhi);
         if (a.lut) {
 #pragma unroll
             for (int i = 0; i < 4; i++) v[i] = lut_s[v[i] + 128];
