@@ -1030,14 +1030,14 @@ static void launch_rows_nt(int nt, int mode, const ConvArgs &a, dim3 grid, size_
 }
 
 // Bytes of dynamic LDS the row-staged kernel needs for one layer.
-// Output pixels per k_conv_rows tile: whole output rows when at least one
-// fits the block's 64*rb pixels (then a tile's input rows overlap its
+// Output pixels per k_conv_rows tile: whole output rows when they fill at
+// least 7/8 of the block's 64*rb pixels (then a tile's input rows overlap its
 // neighbours' only by the kernel's halo), else 64*rb consecutive pixels.
 // Sets *span to the most output rows one tile touches.
 static int rows_tile(const UQKSpatial *d, int rb, int *span)
 {
     const int bm = 4 * 16 * rb, rpt = bm / d->ow;
-    if (rpt >= 1) {
+    if (rpt >= 1 && 8 * rpt * d->ow >= 7 * bm) {
         *span = rpt;
         return rpt * d->ow;
     }
@@ -1101,13 +1101,13 @@ static int conv_launch(const UQKSpatial *d, const void *x, void *y, uint32_t bat
     if (a.M <= 0) return 0;
     const int nchunks = d->oc_pad / (16 * d->nt);
     if (d->mode == UQK_STEM) {
-        // A block is four output rows x one 64-pixel segment per wave (four
-        // row blocks: wider segments cost waves per SIMD, which this
-        // latency-bound kernel needs more); the channel slice covers up to 64
+        // A block is four output rows x one 128-pixel segment per wave
+        // (eight row blocks: rows up to 128 pixels are one segment, so each
+        // input row is staged once); the channel slice covers up to 64
         // channels (NT = oc_pad / 16 when that is 1, 2 or 4).
         const int nt = d->oc_pad == 16 ? 1 : d->oc_pad == 32 ? 2 : 4;
         a.images = (int)batches;
-        a.segs = (d->ow + 63) / 64;
+        a.segs = (d->ow + 127) / 128;
         a.row_groups = (d->oh + 3) / 4;
         a.kw_magic = (65536 + d->kw - 1) / d->kw;
         a.stem_rows = 3 * d->sh + (d->kh - 1) * d->dh + 1;
@@ -1119,10 +1119,10 @@ static int conv_launch(const UQKSpatial *d, const void *x, void *y, uint32_t bat
 #define UQK_STEM_EM(NT)                                                                                    \
     do {                                                                                                   \
         switch (a.emode) {                                                                                 \
-        case 0: hipLaunchKernelGGL((k_conv_stem<4, NT, 0>), grid, dim3(256), lds, g_stream, a); break;     \
-        case 1: hipLaunchKernelGGL((k_conv_stem<4, NT, 1>), grid, dim3(256), lds, g_stream, a); break;     \
-        case 2: hipLaunchKernelGGL((k_conv_stem<4, NT, 2>), grid, dim3(256), lds, g_stream, a); break;     \
-        default: hipLaunchKernelGGL((k_conv_stem<4, NT, 3>), grid, dim3(256), lds, g_stream, a); break;    \
+        case 0: hipLaunchKernelGGL((k_conv_stem<8, NT, 0>), grid, dim3(256), lds, g_stream, a); break;     \
+        case 1: hipLaunchKernelGGL((k_conv_stem<8, NT, 1>), grid, dim3(256), lds, g_stream, a); break;     \
+        case 2: hipLaunchKernelGGL((k_conv_stem<8, NT, 2>), grid, dim3(256), lds, g_stream, a); break;     \
+        default: hipLaunchKernelGGL((k_conv_stem<8, NT, 3>), grid, dim3(256), lds, g_stream, a); break;    \
         }                                                                                                  \
     } while (0)
         if (nt == 1) UQK_STEM_EM(1);
@@ -1645,14 +1645,15 @@ static int launch_dw_win(const UQKSpatial *d, const void *x, void *y, uint32_t b
 // taps past KS*KS carry zero weights. The products and their sum are the
 // signed int8 ones of the dot4 kernel, so the same records requantise them.
 //
-// A block is one image x GB groups of 16 channels (GB = 1, 2 or 4; more for
-// small maps, whose images have few tiles): the padded input window the
-// image's outputs need ((OH-1)*S + KS rows and columns, padding as the zero
-// point) is staged once in LDS, one plane per group, and the 4/GB waves of a
-// group take 16-pixel tiles of the image's flattened output in turn (so 7x7
-// maps waste only the last tile's tail). Blocks are ordered channel groups
-// outer, image inner, so the groups of one image share an XCD (and its L2)
-// when the image count is a multiple of 8.
+// A block is one band of output rows of one image (the whole map when its
+// window fits 40 KiB of LDS) x GB groups of 16 channels (GB = 1, 2 or 4; more
+// for small maps, whose images have few tiles): the padded input window the
+// band's outputs need ((rows-1)*S + KS rows, (OW-1)*S + KS columns, padding
+// as the zero point) is staged once in LDS, one plane per group, and the 4/GB
+// waves of a group take 16-pixel tiles of the band's flattened output in turn
+// (so 7x7 maps waste only the last tile's tail). Blocks are ordered channel
+// groups outer, image and band inner, so the groups of one image share an XCD
+// (and its L2) when the block count per group set is a multiple of 8.
 // ---------------------------------------------------------------------------
 struct DwMArgs {
     const int8_t *x;
@@ -1662,6 +1663,7 @@ struct DwMArgs {
     const uint8_t *lut;
     int ih, iw, c, oh, ow, pt, pl, xz, yz, lo, hi;
     int images, rows_p, cols_p;
+    int band, bands;           // output rows per block, blocks per image and group set
     int lgb, lwg;              // log2 of channel groups per block, of waves per group
     unsigned m_cols, m_ow;     // udiv_magic(cols_p), udiv_magic(ow)
 };
@@ -1674,25 +1676,30 @@ __global__ __launch_bounds__(256) void k_dw_mfma(DwMArgs a)
     __shared__ __attribute__((aligned(4))) int8_t lut_s[256];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;
-    const int gblock = blockIdx.x / a.images, n = blockIdx.x - gblock * a.images;
+    // blockIdx.x = (group set * images + image) * bands + band
+    const int per_set = a.images * a.bands;
+    const int gblock = blockIdx.x / per_set, nb = blockIdx.x - gblock * per_set;
+    const int n = nb / a.bands, oyb = (nb - n * a.bands) * a.band;   // first output row of the band
+    const int brows = min(a.band, a.oh - oyb);
     const int gw = wave >> a.lwg, wsub = wave & ((1 << a.lwg) - 1);   // this wave's group, rank in it
     const int cblk = gblock << (a.lgb + 4), c0 = cblk + gw * 16;
     const int xzw = (a.xz & 0xff) * 0x01010101;
-    const int plane = a.rows_p * a.cols_p;          // staged pixels per group
+    const int plane = a.rows_p * a.cols_p;          // staged pixels per group (a full band)
+    const int iyb = oyb * S - a.pt;                 // input row of staged row 0
 
-    // Stage the padded window: item q = (staged pixel, group) with the group
-    // fastest (one pixel's GB 16-byte chunks are contiguous in HBM); staged
-    // pixel (r, cc) is input (r - pt, cc - pl).
+    // Stage the band's padded window: item q = (staged pixel, group) with the
+    // group fastest (one pixel's GB 16-byte chunks are contiguous in HBM);
+    // staged pixel (r, cc) is input (iyb + r, cc - pl).
     {
         const int8_t *xim = a.x + (long)n * a.ih * a.iw * a.c + cblk;
-        const int total = plane << a.lgb;
+        const int total = (((brows - 1) * S + KS) * a.cols_p) << a.lgb;
         for (int q0 = threadIdx.x; q0 < total; q0 += 4 * 256) {
             v4i v[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int q = q0 + j * 256, sp = q >> a.lgb, gq = q & ((1 << a.lgb) - 1);
                 const int r = (int)udiv((unsigned)sp, (unsigned)a.cols_p, a.m_cols), cc = sp - r * a.cols_p;
-                const int iy = r - a.pt, ix = cc - a.pl;
+                const int iy = iyb + r, ix = cc - a.pl;
                 const bool in = q < total && (unsigned)iy < (unsigned)a.ih && (unsigned)ix < (unsigned)a.iw;
                 v[j] = (v4i){xzw, xzw, xzw, xzw};
                 if (in) v[j] = *(const v4i *)(xim + ((long)iy * a.iw + ix) * a.c + gq * 16);
@@ -1724,13 +1731,13 @@ __global__ __launch_bounds__(256) void k_dw_mfma(DwMArgs a)
     const int vlo = vgpr(a.lo), vhi = vgpr(a.hi);
     __syncthreads();
 
-    const int npix = a.oh * a.ow, tiles = (npix + 15) >> 4;
-    int8_t *yim = a.y + (long)n * npix * a.c + c0;
+    const int npix = brows * a.ow, tiles = (npix + 15) >> 4;   // the band's output pixels
+    int8_t *yim = a.y + ((long)n * a.oh + oyb) * a.ow * a.c + c0;
     const int8_t *pl = smem + (size_t)gw * plane * 16;
     for (int tile = wsub; tile < tiles; tile += 1 << a.lwg) {
-        // A row: output pixel p (clamped into the map for the tail tile).
+        // A row: band pixel p (clamped into the band for the tail tile).
         const int p = min(tile * 16 + lr, npix - 1);
-        const int oy = (int)udiv((unsigned)p, (unsigned)a.ow, a.m_ow), ox = p - oy * a.ow;
+        const int oy = (int)udiv((unsigned)p, (unsigned)a.ow, a.m_ow), ox = p - oy * a.ow;   // oy within the band
         const int8_t *base = pl + (oy * S * a.cols_p + ox * S) * 16;
         v4i A[NG];
 #pragma unroll
@@ -1760,17 +1767,25 @@ static size_t dw_mfma_plan(const UQKSpatial *d, DwMArgs *t)
     if (!d->dwwin || d->oc % 16 || d->ic != d->oc || d->kh != d->kw || (ks != 3 && ks != 5) || d->sh != d->sw ||
         (s != 1 && s != 2) || d->dh != 1 || d->dw != 1)
         return 0;
-    t->rows_p = (d->oh - 1) * s + ks;
     t->cols_p = (d->ow - 1) * s + ks;
+    // Output rows per block: the whole map when its padded window fits 40
+    // KiB, else the most rows whose window does (bands of the map).
+    const size_t row_bytes = (size_t)t->cols_p * 16;
+    int band = d->oh;
+    if ((size_t)((band - 1) * s + ks) * row_bytes > 40960) band = (int)((40960 / row_bytes - ks) / s + 1);
+    if (band < 1 || (size_t)ks * row_bytes > 40960) return 0;
+    t->band = band;
+    t->bands = (d->oh + band - 1) / band;
+    t->rows_p = (band - 1) * s + ks;
     // Groups per block: enough tiles per wave on small maps (a 7x7 image has
     // four), a whole number of blocks per image, the planes within 40 KiB.
-    const int tiles = (d->oh * d->ow + 15) / 16, groups = d->oc / 16;
+    const int tiles = (band * d->ow + 15) / 16, groups = d->oc / 16;
     int lgb = tiles <= 4 ? 2 : tiles <= 16 ? 1 : 0;
     while (lgb && (groups % (1 << lgb) || ((size_t)t->rows_p * t->cols_p * 16 << lgb) > 40960)) lgb--;
     t->lgb = lgb;
     t->lwg = 2 - lgb;
     const size_t bytes = (size_t)t->rows_p * t->cols_p * 16 << lgb;
-    if (bytes > 40960 || (long)d->oh * d->ow >= 65536) return 0;
+    if (bytes > 40960 || (long)band * d->ow >= 65536) return 0;
     t->m_cols = udiv_magic((unsigned)t->cols_p);
     t->m_ow = udiv_magic((unsigned)d->ow);
     return bytes;
@@ -1789,7 +1804,7 @@ static int launch_dw_mfma(const UQKSpatial *d, const void *x, void *y, uint32_t 
     a.ih = d->ih; a.iw = d->iw; a.c = d->oc; a.oh = d->oh; a.ow = d->ow; a.pt = d->pt; a.pl = d->pl;
     a.xz = d->xz; a.yz = d->yz; a.lo = d->lo; a.hi = d->hi;
     a.images = (int)batches;
-    const unsigned long long blocks = (unsigned long long)batches * (d->oc / 16 >> a.lgb);
+    const unsigned long long blocks = (unsigned long long)batches * a.bands * (d->oc / 16 >> a.lgb);
     if (blocks > 0x7fffffffULL || batches == 0) return blocks ? -1 : 0;
     const int mode = (d->hi_shift ? 1 : 0) | (d->corr ? 2 : 0);
 #define UQK_DWM(K, S)                                                                                           \
