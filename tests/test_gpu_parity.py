@@ -233,3 +233,17 @@ def test_snapshot_of_fused_conv_output(lib, name):
         _, want = oracle_run(plan, x, images, P.output_bytes(plan), snap=t, snap_bytes=nbytes)
         _assert_same(g.snapshot_images(t, nbytes), want, f"{name} snapshot tensor {t}")
     _assert_same(g.run_batch(x, images), y, f"{name} rerun after snapshots")
+
+
+def test_gather_conv_with_fused_add(lib):
+    """A 3x3 conv too wide for row staging (80x80x128, K = 1152: the gather
+    kernel) followed by a residual add of its input: the add runs in the
+    gather kernel's epilogue; the same kernel without an add (the conv3x3
+    workload) must not touch the add's table."""
+    p = P.Plan(31)
+    x = p.input((1, 80, 80, 128), zp=5)
+    y = p.conv(x, 128, k=3, act="relu", shift=(-12, -4))
+    plan = p.build(p.add(y, x, act="none"))
+    images = 2
+    xin = P.random_input(plan, images, 12)
+    _assert_same(Graph(plan, lib).run_batch(xin, images), _oracle(plan, xin, images), "gather conv + add")

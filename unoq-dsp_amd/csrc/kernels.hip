@@ -552,7 +552,7 @@ __host__ __device__ inline size_t conv_lds(int kpad, int rb, int nt)
     return w > st ? w : st;
 }
 
-template <int RB, int NT, int MODE, int EMODE>
+template <int RB, int NT, int MODE, int EMODE, bool ADD>
 __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
 {
     constexpr int R = RB * 16;
@@ -561,7 +561,7 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     __shared__ __attribute__((aligned(4))) int8_t lut_s[256];
     __shared__ int4 epi_s[2 * NT * 16];
-    __shared__ int add_s[512];
+    __shared__ int add_s[ADD ? 512 : 1];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;
@@ -608,8 +608,8 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
         }
     }
     const ConstRegs consts = consts_load<NT>(a, n0);
-    int rw[RB][NT];
-    load_residual<RB, NT>(a, rw, row0, a.M, n0, lane);
+    int rw[RB][NT] = {};
+    if (ADD) load_residual<RB, NT>(a, rw, row0, a.M, n0, lane);
     v4i acc[RB][NT];
 #pragma unroll
     for (int rb = 0; rb < RB; rb++)
@@ -659,14 +659,18 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
             }
         }
     }
+    // ADD instances may also run layers without a fused add (the gather
+    // modes have no ADD = false instance): the table and residual exist only
+    // when a.res is set.
+    const bool fused = ADD && a.res != nullptr;
     consts_store<NT>(a, consts, epi_s, lut_s);
-    if (a.res) {
+    if (fused) {
         add_s[threadIdx.x] = a.add_tab[threadIdx.x];
         add_s[256 + threadIdx.x] = a.add_tab[256 + threadIdx.x];
     }
     __syncthreads();
     conv_epilogue_em<RB, NT, EMODE>(a, acc, smem + wave * R * STRIDE, n0, lane, row0, a.M, epi_s, lut_s,
-                                    a.res ? add_s : nullptr, rw);
+                                    fused ? add_s : nullptr, rw);
 }
 
 // Spatial conv with the block's input rows staged in LDS. A block covers BM =
@@ -977,17 +981,24 @@ static void launch_conv_mode(int mode, const ConvArgs &a, dim3 grid, size_t)
     const size_t lds = conv_lds(a.kpad, RB, NT);
     switch (mode) {
     case UQK_PW:
-        // The common case: one kernel per requantisation variant.
-        switch (a.emode) {
-        case 0: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 0>), grid, dim3(256), lds, g_stream, a); break;
-        case 1: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 1>), grid, dim3(256), lds, g_stream, a); break;
-        case 2: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 2>), grid, dim3(256), lds, g_stream, a); break;
-        default: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 3>), grid, dim3(256), lds, g_stream, a); break;
-        }
+        // The common case: one kernel per requantisation variant and per
+        // presence of a fused add.
+#define UQK_PW_EM(ADD)                                                                                          \
+    do {                                                                                                        \
+        switch (a.emode) {                                                                                      \
+        case 0: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 0, ADD>), grid, dim3(256), lds, g_stream, a); break;  \
+        case 1: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 1, ADD>), grid, dim3(256), lds, g_stream, a); break;  \
+        case 2: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 2, ADD>), grid, dim3(256), lds, g_stream, a); break;  \
+        default: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 3, ADD>), grid, dim3(256), lds, g_stream, a); break; \
+        }                                                                                                       \
+    } while (0)
+        if (a.res) UQK_PW_EM(true);
+        else UQK_PW_EM(false);
+#undef UQK_PW_EM
         break;
-    case UQK_G16: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G16, -1>), grid, dim3(256), lds, g_stream, a); break;
-    case UQK_G4: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G4, -1>), grid, dim3(256), lds, g_stream, a); break;
-    default: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G1, -1>), grid, dim3(256), lds, g_stream, a); break;
+    case UQK_G16: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G16, -1, true>), grid, dim3(256), lds, g_stream, a); break;
+    case UQK_G4: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G4, -1, true>), grid, dim3(256), lds, g_stream, a); break;
+    default: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G1, -1, true>), grid, dim3(256), lds, g_stream, a); break;
     }
 }
 
