@@ -680,7 +680,7 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
 // WORDS: IC % 16 != 0. Each staged pixel holds icp = IC rounded up to four
 // bytes (the extra channels are zero, and so are their weights), K counts
 // icp-wide taps, and an A slice is four aligned 4-byte LDS reads.
-template <int RB, int NT, bool WORDS, int EMODE>
+template <int RB, int NT, bool WORDS, int EMODE, bool DIRECT>
 __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
 {
     constexpr int R = RB * 16;
@@ -833,11 +833,13 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
                     A[rb] = (v4i){r4[0], r4[1], r4[2], r4[3]};
                 }
             }
+            // DIRECT: channels as the MFMA rows, for the register-direct store.
 #pragma unroll
             for (int nt = 0; nt < NT; nt++)
 #pragma unroll
                 for (int rb = 0; rb < RB; rb++)
-                    acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[rb], B[p][nt], acc[rb][nt], 0, 0, 0);
+                    acc[rb][nt] = DIRECT ? __builtin_amdgcn_mfma_i32_16x16x64_i8(B[p][nt], A[rb], acc[rb][nt], 0, 0, 0)
+                                         : __builtin_amdgcn_mfma_i32_16x16x64_i8(A[rb], B[p][nt], acc[rb][nt], 0, 0, 0);
             if (s + P < steps) {
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) B[p][nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad + (s + P) * 64);
@@ -845,9 +847,14 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
         }
     }
     const long img0 = n * a.ohw;
-    const int rw[RB][NT] = {};
-    conv_epilogue_em<RB, NT, EMODE>(a, acc, stage, n0, lane, img0 + p0 + wave * R, img0 + pend, epi_s, lut_s,
-                                    nullptr, rw);
+    if constexpr (DIRECT) {
+        conv_store_direct<RB, NT, (EMODE & 1) != 0, (EMODE & 2) != 0>(a, acc, n0, lane, img0 + p0 + wave * R,
+                                                                       img0 + pend, epi_s, lut_s);
+    } else {
+        const int rw[RB][NT] = {};
+        conv_epilogue_em<RB, NT, EMODE>(a, acc, stage, n0, lane, img0 + p0 + wave * R, img0 + pend, epi_s, lut_s,
+                                        nullptr, rw);
+    }
 }
 
 // Stem convolution: at most four input channels and 16 taps (kh * kw), so
@@ -1016,13 +1023,16 @@ static void launch_conv_nt(int nt, int mode, const ConvArgs &a, dim3 grid, size_
 template <int RB>
 static void launch_rows_nt(int nt, int mode, const ConvArgs &a, dim3 grid, size_t lds)
 {
+    // Register-direct epilogue (no LDS output stage) with four row blocks;
+    // uqk_conv picks rb = 4 only when OC % 16 == 0 (whole 16-byte stores).
+    constexpr bool DIR = RB % 4 == 0;
 #define UQK_ROWS_EM(NT, W)                                                                                      \
     do {                                                                                                        \
         switch (a.emode) {                                                                                      \
-        case 0: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 0>), grid, dim3(256), lds, g_stream, a); break;      \
-        case 1: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 1>), grid, dim3(256), lds, g_stream, a); break;      \
-        case 2: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 2>), grid, dim3(256), lds, g_stream, a); break;      \
-        default: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 3>), grid, dim3(256), lds, g_stream, a); break;     \
+        case 0: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 0, DIR>), grid, dim3(256), lds, g_stream, a); break; \
+        case 1: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 1, DIR>), grid, dim3(256), lds, g_stream, a); break; \
+        case 2: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 2, DIR>), grid, dim3(256), lds, g_stream, a); break; \
+        default: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 3, DIR>), grid, dim3(256), lds, g_stream, a); break; \
         }                                                                                                       \
     } while (0)
 #define UQK_ROWS_LAUNCH(NT)                                                                                     \
@@ -1056,17 +1066,23 @@ static int rows_tile(const UQKSpatial *d, int rb, int *span)
     return bm;
 }
 
-extern "C" size_t uqk_conv_rows_lds(const UQKSpatial *d, int rb)
+// Dynamic LDS of k_conv_rows at rb row blocks per wave: the staged tile, the
+// offset table and, unless the epilogue stores straight from registers
+// (rb = 4, OC % 16 == 0), the output stage.
+static size_t rows_lds(const UQKSpatial *d, int rb)
 {
     int span;
     rows_tile(d, rb, &span);
+    const bool direct = rb % 4 == 0 && d->oc % 16 == 0;
     const int rows_max = (span - 1) * d->sh + (d->kh - 1) * d->dh + 1;
     const int cols = (d->ow - 1) * d->sw + (d->kw - 1) * d->dw + 1;
     const int ndelta = d->mode == UQK_ROWS16 ? d->K / 16 : d->K / 4;
     const int icp = d->mode == UQK_ROWS16 ? d->ic : (d->ic + 3) & ~3;
     return (size_t)((rows_max * cols * icp + 15) & ~15) + (size_t)((ndelta * 4 + 15) & ~15) +
-           (size_t)4 * 16 * rb * (16 * d->nt + 16);
+           (direct ? 0 : (size_t)4 * 16 * rb * (16 * d->nt + 16));
 }
+
+extern "C" size_t uqk_conv_rows_lds(const UQKSpatial *d, int rb) { return rows_lds(d, rb); }
 
 static int conv_launch(const UQKSpatial *d, const void *x, void *y, uint32_t batches, const UQKAdd *add);
 
@@ -1145,7 +1161,7 @@ static int conv_launch(const UQKSpatial *d, const void *x, void *y, uint32_t bat
     }
     if (d->mode == UQK_ROWS16 || d->mode == UQK_ROWS4) {
         // Larger tiles stage fewer redundant input rows per output row.
-        const int rb = d->nt <= 4 && uqk_conv_rows_lds(d, 4) <= 65536 ? 4 : 2;
+        const int rb = d->nt <= 4 && d->oc % 16 == 0 && rows_lds(d, 4) <= 65536 ? 4 : 2;
         int span;
         a.tile_px = rows_tile(d, rb, &span);
         a.tiles = (a.ohw + a.tile_px - 1) / a.tile_px;
