@@ -1084,8 +1084,7 @@ static int enqueue_op(uint32_t i, uint32_t images)
             for (uint32_t d = 0; d < axis; d++) outer *= a->d[d];
             for (uint32_t d = axis + 1; d < a->rank; d++) inner *= a->d[d];
             size_t ac = (size_t)a->d[axis] * inner, bc = (size_t)b->d[axis] * inner;
-            rc = uqk_d2d_2d(zp, ac + bc, ap, ac, ac, outer);
-            if (!rc) rc = uqk_d2d_2d((uint8_t *)zp + ac, ac + bc, bp, bc, bc, outer);
+            rc = uqk_rows2(zp, ac + bc, ap, ac, ac, bp, bc, bc, outer);
             break;
         }
         case 21: rc = uqk_resize(ap, zp, images * a->d[0], a->d[1], a->d[2], z->d[1], z->d[2], a->d[3], bp); break;
@@ -1104,7 +1103,14 @@ static int enqueue_op(uint32_t i, uint32_t images)
                 out[lead + d] = z->d[d];
                 off[lead + d] = -(int32_t)o->p[d];
             }
-            rc = uqk_window4(ap, zp, images, in, out, off, 0);
+            /* A slice of the last axis only, inside it, is a row copy (other
+             * windows fill positions outside the input). */
+            if (in[0] == out[0] && in[1] == out[1] && in[2] == out[2] && !off[0] && !off[1] && !off[2] &&
+                off[3] <= 0 && (int64_t)out[3] - off[3] <= (int64_t)in[3])
+                rc = uqk_rows2(zp, out[3], (const uint8_t *)ap - off[3], in[3], out[3], NULL, 0, 0,
+                               (uint64_t)images * in[0] * in[1] * in[2]);
+            else
+                rc = uqk_window4(ap, zp, images, in, out, off, 0);
             break;
         }
         case 19: {
@@ -1116,7 +1122,8 @@ static int enqueue_op(uint32_t i, uint32_t images)
                     for (uint32_t k = 0; k < images && !rc; k++)
                         rc = uqk_d2d((uint8_t *)zp + (size_t)k * z->bytes + off, G.ptr[list[j]], t->bytes);
                 } else
-                    rc = uqk_d2d_2d((uint8_t *)zp + off, z->bytes, G.ptr[list[j]], t->bytes, t->bytes, images);
+                    rc = uqk_rows2((uint8_t *)zp + off, z->bytes, G.ptr[list[j]], t->bytes, t->bytes, NULL, 0, 0,
+                                   images);
                 off += t->bytes;
             }
             break;

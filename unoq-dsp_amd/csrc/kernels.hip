@@ -13,6 +13,7 @@
 //   * depthwise (code 15) and pooling (code 16) are bandwidth kernels on the
 //     vector ALU; add/mean/LUT/resize/pad/slice are byte-movement kernels.
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 #include "uqk.h"
 
@@ -673,9 +674,10 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
                                     fused ? add_s : nullptr, rw);
 }
 
-// Spatial conv with the block's input rows staged in LDS. A block covers BM =
-// 4*RB*16 consecutive output pixels of one image (tiles never straddle
-// images); the staged region is the rows those pixels touch, full width, with
+// Spatial conv with the block's input rows staged in LDS. A block covers up
+// to 4*RB*16 consecutive output pixels of one image (a.tile_px: whole output
+// rows where they fill the block well; tiles never straddle images); the
+// staged region is the rows those pixels touch, full width, with
 // out-of-image positions written as xz so the K loop has no bounds checks.
 // WORDS: IC % 16 != 0. Each staged pixel holds icp = IC rounded up to four
 // bytes (the extra channels are zero, and so are their weights), K counts
@@ -684,7 +686,6 @@ template <int RB, int NT, bool WORDS, int EMODE, bool DIRECT>
 __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
 {
     constexpr int R = RB * 16;
-    constexpr int BM = 4 * R;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     __shared__ __attribute__((aligned(4))) int8_t lut_s[256];
     __shared__ int4 epi_s[2 * NT * 16];
@@ -2441,6 +2442,60 @@ extern "C" int uqk_window4(const void *x, void *y, uint32_t images, const uint32
     if (!total) return 0;
     hipLaunchKernelGGL(k_window4, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g_stream,
                        (const int8_t *)x, (int8_t *)y, total, g, fill, in_bytes, out_bytes);
+    UQK_LAUNCHED();
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Row copies: destination row r (pitch dp) = row r of source 1 (w1 bytes at
+// pitch s1) followed by row r of source 2 (w2 bytes at pitch s2, w2 may be
+// 0). Concatenation (code 20), packing (19) and channel slices (26) are all
+// this pattern. V-byte chunks (16, 4 or 1: whatever every pointer, pitch and
+// width allows), one per thread; chunk q -> (row, chunk) by a 64-bit
+// multiply-high, exact for q < 2^32.
+// ---------------------------------------------------------------------------
+struct Rows2 {
+    int8_t *y;
+    const int8_t *a, *b;
+    uint64_t dp, s1, s2;       // pitches in bytes
+    uint32_t c1, cpr;          // chunks of source 1 per row, chunks per destination row
+    uint64_t magic;            // ceil(2^64 / cpr), 0 when cpr == 1
+    uint64_t total;            // chunks
+};
+
+template <int V>
+__global__ __launch_bounds__(256) void k_rows2(Rows2 g)
+{
+    typedef typename std::conditional<V == 16, v4i, typename std::conditional<V == 4, int, int8_t>::type>::type T;
+    const uint64_t q = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (q >= g.total) return;
+    const uint64_t row = g.cpr == 1 ? q : __umul64hi(q, g.magic);
+    const uint32_t c = (uint32_t)(q - row * g.cpr);
+    T v;
+    if (c < g.c1) v = *(const T *)(g.a + row * g.s1 + (uint64_t)c * V);
+    else v = *(const T *)(g.b + row * g.s2 + (uint64_t)(c - g.c1) * V);
+    *(T *)(g.y + row * g.dp + (uint64_t)c * V) = v;
+}
+
+extern "C" int uqk_rows2(void *y, uint64_t dp, const void *a, uint64_t s1, uint64_t w1, const void *b, uint64_t s2,
+                         uint64_t w2, uint64_t rows)
+{
+    if (!rows || !(w1 + w2)) return 0;
+    const uint64_t bits = (uint64_t)(uintptr_t)y | dp | (uint64_t)(uintptr_t)a | s1 | w1 |
+                          (w2 ? ((uint64_t)(uintptr_t)b | s2 | w2) : 0);
+    const int V = (bits & 15) == 0 ? 16 : (bits & 3) == 0 ? 4 : 1;
+    Rows2 g;
+    g.y = (int8_t *)y; g.a = (const int8_t *)a; g.b = (const int8_t *)b;
+    g.dp = dp; g.s1 = s1; g.s2 = s2;
+    g.c1 = (uint32_t)(w1 / V);
+    g.cpr = (uint32_t)((w1 + w2) / V);
+    g.magic = g.cpr == 1 ? 0 : ~0ULL / g.cpr + 1;
+    g.total = rows * g.cpr;
+    if (g.total >> 32) return (int)hipErrorInvalidValue;
+    const dim3 grid((unsigned)((g.total + 255) / 256));
+    if (V == 16) hipLaunchKernelGGL(k_rows2<16>, grid, dim3(256), 0, g_stream, g);
+    else if (V == 4) hipLaunchKernelGGL(k_rows2<4>, grid, dim3(256), 0, g_stream, g);
+    else hipLaunchKernelGGL(k_rows2<1>, grid, dim3(256), 0, g_stream, g);
     UQK_LAUNCHED();
     return 0;
 }

@@ -84,6 +84,10 @@ int uqk_h2d(void *dst, const void *src, size_t bytes);        /* async on the st
 int uqk_d2h(void *dst, const void *src, size_t bytes);        /* async on the stream */
 int uqk_d2d(void *dst, const void *src, size_t bytes);        /* async on the stream */
 int uqk_d2d_2d(void *dst, size_t dpitch, const void *src, size_t spitch, size_t width, size_t height);
+/* rows copies: y row r (pitch dp) = a row r (w1 bytes, pitch s1) then b row r
+ * (w2 bytes, pitch s2; w2 may be 0). One kernel launch. */
+int uqk_rows2(void *y, uint64_t dp, const void *a, uint64_t s1, uint64_t w1, const void *b, uint64_t s2, uint64_t w2,
+              uint64_t rows);
 int uqk_sync(void);
 int uqk_last_error(void);
 
