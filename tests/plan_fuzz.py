@@ -255,3 +255,81 @@ def conv_add_bytes_plan(seed):
     r = p.conv(t, c, k=1, act="none", shift=(-12, -4))
     z = p.add(y, r) if _pick(rng, [0, 1]) else p.add(r, y)
     return p.build(z)
+
+
+def dw_mfma_plan(seed):
+    """A depthwise layer the matrix-core kernel takes: 3x3 or 5x5, stride 1
+    or 2, 16-64 channels, maps from 3x3 to banded sizes (padded windows over
+    40 KiB), SAME or explicit padding, optional post table, both
+    requantisation ranges."""
+    rng = Rng(seed, 717171)
+    p = Plan(seed)
+    hw = _pick(rng, [3, 5, 7, 9, 14, 17, 28, 33, 56, 80])
+    c = _pick(rng, [16, 32, 48, 64])
+    n = 1 if hw >= 56 else _pick(rng, [1, 2])
+    x = p.input((n, hw, hw, c), zp=int(rng.integers(1, -128, 127)[0]))
+    k = _pick(rng, [3, 5])
+    stride = _pick(rng, [1, 2])
+    if _pick(rng, [0, 1]):
+        padding = "same"
+    else:
+        pt, pb = _geometry(rng, hw, k, stride, 1)
+        padding = (pt, pt, pb, pb)
+    lut = _random_lut(p, rng) if _pick(rng, [0, 0, 1]) else None
+    lo = int(rng.integers(1, -24, -1)[0])
+    for shift in ((lo, 3), (-12, -4), (-20, -1)):
+        try:
+            y = p.depthwise(x, k=k, stride=stride, padding=padding, act=_pick(rng, ["none", "relu", "relu6"]),
+                            q6=int(rng.integers(1, 1, 200)[0]), lut=lut, shift=shift,
+                            zero_mult=_pick(rng, [0.0, 0.3]), w_sigma=_pick(rng, [3, 40, 90]),
+                            bias_sigma=_pick(rng, [0, 2048, 60000]))
+            return p.build(y)
+        except ValueError:
+            continue
+    raise AssertionError("unreachable")
+
+
+def stem_plan(seed):
+    """A stem conv (IC 1-4, kh*kw <= 16, OC a multiple of 16): widths past 128
+    output columns (several row segments), strides 1-2, odd sizes."""
+    rng = Rng(seed, 818181)
+    p = Plan(seed)
+    ic = _pick(rng, [1, 2, 3, 4])
+    w = _pick(rng, [16, 32, 48, 64, 96, 160, 272])
+    h = _pick(rng, [5, 9, 16, 23])
+    x = p.input((1, h, w, ic), zp=int(rng.integers(1, -128, 127)[0]))
+    k = _pick(rng, [1, 2, 3, 3, 4])
+    stride = _pick(rng, [1, 2, 2])
+    lut = _random_lut(p, rng) if _pick(rng, [0, 0, 1]) else None
+    lo = int(rng.integers(1, -24, -1)[0])
+    for shift in ((lo, 3), (-12, -4), (-20, -1)):
+        try:
+            y = p.conv(x, _pick(rng, [16, 32, 48, 64]), k=k, stride=stride, padding=_pick(rng, ["same", (0, 0, 0, 0)]),
+                       act=_pick(rng, ["none", "relu", "relu6"]), q6=int(rng.integers(1, 1, 200)[0]), lut=lut,
+                       shift=shift, w_sigma=_pick(rng, [3, 40, 90]), tail_weights=bool(_pick(rng, [0, 1])))
+            return p.build(y)
+        except ValueError:
+            continue
+    raise AssertionError("unreachable")
+
+
+def rows_conv_plan(seed):
+    """A spatial conv on 16-channel multiples with OC a multiple of 16 and at
+    most 64 channels per slice: the row-staged kernel at four row blocks with
+    its register-direct epilogue; widths whose rows do and do not fill a
+    block."""
+    rng = Rng(seed, 919191)
+    p = Plan(seed)
+    ic = _pick(rng, [16, 32])
+    w = _pick(rng, [7, 14, 20, 28, 56, 60])
+    x = p.input((1, _pick(rng, [4, 9, 14]), w, ic), zp=int(rng.integers(1, -128, 127)[0]))
+    lo = int(rng.integers(1, -24, -1)[0])
+    for shift in ((lo, 3), (-12, -4)):
+        try:
+            y = p.conv(x, _pick(rng, [16, 32, 64]), k=_pick(rng, [3, 3, 5]), stride=_pick(rng, [1, 2]),
+                       act=_pick(rng, ["none", "relu"]), shift=shift, lut=_random_lut(p, rng) if _pick(rng, [0, 1]) else None,
+                       w_sigma=_pick(rng, [3, 40, 90]), tail_weights=bool(_pick(rng, [0, 1])))
+            return p.build(y)
+        except ValueError:
+            continue
+    raise AssertionError("unreachable")

@@ -10,7 +10,8 @@ import pytest
 
 import uq_plan as P
 import uq_workloads as W
-from plan_fuzz import ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, random_plan
+from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, dw_mfma_plan, random_plan,
+                       rows_conv_plan, stem_plan)
 from test_oracle_vs_reference import (BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, softmax_table_plan,
                                       transpose_plan)
 from refs import oracle_run
@@ -247,3 +248,15 @@ def test_gather_conv_with_fused_add(lib):
     images = 2
     xin = P.random_input(plan, images, 12)
     _assert_same(Graph(plan, lib).run_batch(xin, images), _oracle(plan, xin, images), "gather conv + add")
+
+
+@pytest.mark.parametrize("maker", [dw_mfma_plan, stem_plan, rows_conv_plan])
+@pytest.mark.parametrize("seed", range(40))
+def test_kernel_shape_fuzz(lib, maker, seed):
+    """Matrix-core depthwise (bands, channel groups, small maps), the stem
+    (several row segments, IC 1-4) and the row-staged conv with its
+    register-direct epilogue, byte for byte against the oracle."""
+    plan = maker(seed)
+    images = 2
+    x = P.random_input(plan, images, seed)
+    _assert_same(Graph(plan, lib).run_batch(x, images), _oracle(plan, x, images), f"{maker.__name__} {seed}")
