@@ -236,6 +236,37 @@ def test_snapshot_of_fused_conv_output(lib, name):
     _assert_same(g.run_batch(x, images), y, f"{name} rerun after snapshots")
 
 
+@pytest.mark.parametrize("name,images", [("mnv4", 131), ("yolo", 130)])
+def test_split_batch_matches_single_stream(lib, monkeypatch, name, images):
+    """A batch run as two image slices on two streams (uneven slices here)
+    gives the single-stream bytes through both entry points, the images on
+    either side of the slice boundary match the oracle, and a snapshot of a
+    fused conv's output after the split run covers the whole batch."""
+    plan, _ = W.WORKLOADS[name]()
+    x = P.random_input(plan, images, 17)
+    recs = P.tensor_records(plan)
+    targets = _fused_conv_outputs(plan)[:2]
+    outs, snaps = {}, {}
+    for streams in ("1", "2"):
+        monkeypatch.setenv("UQ_STREAMS", streams)
+        g = Graph(plan, lib)
+        outs[streams] = g.run_batch(x, images)
+        snaps[streams] = [g.snapshot_images(t, images * recs[t][1]) for t in targets]
+        din = DeviceBuffer(lib, x.nbytes)
+        dout = DeviceBuffer(lib, images * g.output_bytes)
+        din.upload(x)
+        assert lib.ug_run_device(din.ptr, dout.ptr, images) == 0
+        _assert_same(dout.download(), outs[streams], f"{name} device path, {streams} stream(s)")
+        din.free()
+        dout.free()
+    _assert_same(outs["2"], outs["1"], f"{name} two slices vs one stream")
+    for t, a, b in zip(targets, snaps["2"], snaps["1"]):
+        _assert_same(a, b, f"{name} snapshot of tensor {t} after the split run")
+    ib, ob = P.input_bytes(plan), P.output_bytes(plan)
+    for i in (0, images // 2 - 1, images // 2, images - 1):
+        _assert_same(outs["2"][i * ob:(i + 1) * ob], _oracle(plan, x[i * ib:(i + 1) * ib], 1), f"{name} image {i}")
+
+
 def test_gather_conv_with_fused_add(lib):
     """A 3x3 conv too wide for row staging (80x80x128, K = 1152: the gather
     kernel) followed by a residual add of its input: the add runs in the

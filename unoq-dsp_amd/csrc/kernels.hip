@@ -19,9 +19,12 @@
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-static hipStream_t g_stream;      // compute (and the single-stream entry points)
+static hipStream_t g_stream;      // stream of the next launch: g_main, or a side stream of a split batch
+static hipStream_t g_main;        // compute (and the single-stream entry points)
 static hipStream_t g_copy[2];     // host transfers of the pipelined batch: in, out
 static hipEvent_t g_pipe_ev[8];   // pipeline hand-offs between the three streams
+static hipStream_t g_side[UQK_MAX_SLICES - 1];   // compute streams of the other image slices
+static hipEvent_t g_fork, g_join[UQK_MAX_SLICES - 1];
 static int g_ready;
 static int g_err;
 static hipEvent_t *g_events;
@@ -115,7 +118,9 @@ struct ConvArgs {
     long M;
     int ih, iw, ic, icp, oh, ow, oc, kh, sh, sw, dh, pt, pl, xz, yz, lo, hi, K, kpad, ohw, corr, emode;
     int kw, dw, taps;
-    int images, segs, row_groups, kw_magic, stem_rows;   // stem grid, tap decomposition, staged rows
+    int images, segs, row_groups, seg_rb, stem_rows;     // stem grid: segments, row blocks each, staged rows
+    int stem_cpr;                                        // stem: 16-byte LDS chunks per staged row
+    unsigned stem_cpr_magic;
     int tiles, cols, rows_max, tile_px;
     unsigned m_row, m_px;      // k_conv_rows staging: udiv_magic of items per staged row, per pixel
     // Fused residual add (k_conv only; res == nullptr when there is none).
@@ -420,16 +425,21 @@ __device__ __forceinline__ void rows_transpose4(int (&r)[4])
 // go through rows_transpose4, after which row j of the wave holds all 16
 // channels of one pixel of row block rb0 + j: one 16-byte store per lane, no
 // LDS round trip. Only one tile's four channel records and four words are
-// live at a time. Needs OC % 16 == 0.
-template <int RB, int NT, bool HI, bool CORR>
+// live at a time. Only the first NRB row blocks (at most RB) are
+// requantised and stored. row_base is wave-uniform and rows are at most
+// 2^24 apart within a wave, so the per-lane part of the address is a 24-bit
+// multiply. Needs OC % 16 == 0.
+template <int RB, int NT, bool HI, bool CORR, int NRB = RB>
 __device__ __forceinline__ void conv_store_direct(const ConvArgs &a, const v4i (&acc)[RB][NT], int n0, int lane,
                                                   long row_base, long row_limit, const int4 *epi_s,
                                                   const int8_t *lut_s)
 {
-    static_assert(RB % 4 == 0, "row blocks go through the transpose in fours");
+    static_assert(RB % 4 == 0 && NRB <= RB, "row blocks go through the transpose in fours");
     const int lr = lane & 15, lg = lane >> 4;
     const int vlo = vgpr(a.lo), vhi = vgpr(a.hi);
     const bool lut = a.lut != nullptr;
+    int8_t *ybase = a.y + row_base * a.oc;
+    const int rows_left = row_limit - row_base < (long)(NRB * 16) ? (int)(row_limit - row_base) : NRB * 16;
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         const int cb = n0 + nt * 16;
@@ -437,10 +447,14 @@ __device__ __forceinline__ void conv_store_direct(const ConvArgs &a, const v4i (
 #pragma unroll
         for (int i = 0; i < 4; i++) e[i] = load_epi(epi_s, nt * 16 + 4 * lg + i);
 #pragma unroll
-        for (int rb0 = 0; rb0 < RB; rb0 += 4) {
+        for (int rb0 = 0; rb0 < NRB; rb0 += 4) {
             int r[4];
 #pragma unroll
             for (int q = 0; q < 4; q++) {
+                if (rb0 + q >= NRB) {
+                    r[q] = 0;
+                    continue;
+                }
                 int v[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[rb0 + q][nt][i], e[i], a.yz, vlo, vhi);
@@ -451,8 +465,9 @@ __device__ __forceinline__ void conv_store_direct(const ConvArgs &a, const v4i (
                 r[q] = pack4(v[0], v[1], v[2], v[3]);
             }
             rows_transpose4(r);
-            const long row = row_base + (rb0 + lg) * 16 + lr;
-            if (row < row_limit && cb < a.oc) *(v4i *)(a.y + row * a.oc + cb) = (v4i){r[0], r[1], r[2], r[3]};
+            const int prow = (rb0 + lg) * 16 + lr;
+            if (prow < rows_left && cb < a.oc)
+                *(v4i *)(ybase + __mul24(prow, a.oc) + cb) = (v4i){r[0], r[1], r[2], r[3]};
         }
     }
 }
@@ -711,22 +726,25 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
     // Staging: each thread issues STAGE_U loads before its first LDS write,
     // so a block waits for about one HBM latency, not one per staged row.
     constexpr int STAGE_U = 4;
-    // Staged item q -> (row, column, channel offset) by multiply-high (q,
-    // the row width and the pixel width are all below 2^16).
+    // Staged item q -> (row, 16-byte piece) by multiply-high (q and the row
+    // width are below 2^16). A piece never straddles pixels (IC % 16 == 0),
+    // so its input byte is linear in the piece: b16 * 16 - pl * IC of the
+    // input row, inside the image when that is in [0, IW * IC).
     if (!WORDS) {
         const int xzw = (a.xz & 0xff) * 0x01010101;
-        const int cpr = rowbytes >> 4, total = rows * cpr, ic16 = a.ic >> 4;
+        const int cpr = rowbytes >> 4, total = rows * cpr;
+        const int in_row = a.iw * a.ic, lead = a.pl * a.ic;
+        const int8_t *xrow = xim + (long)iy_lo * in_row;
         for (int q0 = threadIdx.x; q0 < total; q0 += STAGE_U * 256) {
             v4i v[STAGE_U];
 #pragma unroll
             for (int j = 0; j < STAGE_U; j++) {
                 const int q = q0 + j * 256;
-                const int r = (int)udiv((unsigned)q, (unsigned)cpr, a.m_row), b16 = q - r * cpr;
-                const int col = (int)udiv((unsigned)b16, (unsigned)ic16, a.m_px), c = (b16 - col * ic16) << 4;
-                const int iy = iy_lo + r, ix = col - a.pl;
+                const int r = (int)udiv((unsigned)q, (unsigned)cpr, a.m_row);
+                const int off = ((q - __mul24(r, cpr)) << 4) - lead;
+                const bool in = q < total && (unsigned)(iy_lo + r) < (unsigned)a.ih && (unsigned)off < (unsigned)in_row;
                 v[j] = (v4i){xzw, xzw, xzw, xzw};
-                if (q < total && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw)
-                    v[j] = *(const v4i *)(xim + ((long)iy * a.iw + ix) * a.ic + c);
+                if (in) v[j] = *(const v4i *)(xrow + __mul24(r, in_row) + off);
             }
 #pragma unroll
             for (int j = 0; j < STAGE_U; j++)
@@ -764,12 +782,10 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
     __syncthreads();
 
     int lbase[RB];
-    bool valid[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
         const int p = p0 + wave * R + rb * 16 + lr;
-        valid[rb] = p < pend;
-        const int pp = valid[rb] ? p : p0;
+        const int pp = p < pend ? p : p0;
         const int oy = pp / a.ow, ox = pp - oy * a.ow;
         lbase[rb] = ((oy - oy_a) * a.sh * a.cols + ox * a.sw) * a.icp;
     }
@@ -800,39 +816,24 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
             const int s = s0 + p;
             if (s >= steps) break;
             const int kg = s * 64 + lg * 16;
-            // The K slice's LDS offsets are shared by the row blocks; reads
-            // are unconditional (every lbase is a valid pixel of the tile,
-            // slices past K read offset 0) and invalid rows or slices are
-            // zeroed afterwards, so no LDS round trip waits inside a branch.
+            // The K slice's LDS offsets are shared by the row blocks. Every
+            // read is in the tile (every lbase is a pixel of the tile, slices
+            // past K read offset 0) and used as read: the weights of slices
+            // past K are zero, and rows past the tile are never stored.
             v4i A[RB];
             if (!WORDS) {
-                const bool kin = kg < a.K;
-                const int d = dl[kin ? kg >> 4 : 0];
+                const int d = dl[kg < a.K ? kg >> 4 : 0];
 #pragma unroll
-                for (int rb = 0; rb < RB; rb++) {
-                    const v4i v = *(const v4i *)(xt + lbase[rb] + d);
-                    const bool use = kin && valid[rb];
-                    A[rb] = (v4i){use ? v[0] : 0, use ? v[1] : 0, use ? v[2] : 0, use ? v[3] : 0};
-                }
+                for (int rb = 0; rb < RB; rb++) A[rb] = *(const v4i *)(xt + lbase[rb] + d);
             } else {
                 const int w0 = kg >> 2;
                 int d[4];
-                bool win[4];
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    win[j] = kg < a.K && w0 + j < ndelta;
-                    d[j] = dl[win[j] ? w0 + j : 0];
-                }
+                for (int j = 0; j < 4; j++) d[j] = dl[kg < a.K && w0 + j < ndelta ? w0 + j : 0];
 #pragma unroll
-                for (int rb = 0; rb < RB; rb++) {
-                    int r4[4];
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const int v = *(const int *)(xt + lbase[rb] + d[j]);
-                        r4[j] = win[j] && valid[rb] ? v : 0;
-                    }
-                    A[rb] = (v4i){r4[0], r4[1], r4[2], r4[3]};
-                }
+                for (int rb = 0; rb < RB; rb++)
+                    A[rb] = (v4i){*(const int *)(xt + lbase[rb] + d[0]), *(const int *)(xt + lbase[rb] + d[1]),
+                                  *(const int *)(xt + lbase[rb] + d[2]), *(const int *)(xt + lbase[rb] + d[3])};
             }
             // DIRECT: channels as the MFMA rows, for the register-direct store.
 #pragma unroll
@@ -858,127 +859,126 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
     }
 }
 
-// Stem convolution: at most four input channels and 16 taps (kh * kw), so
-// the receptive field of an output pixel, with every tap widened to a 4-byte
-// word, is a single 64-byte K step. A block is four waves on four consecutive
-// output rows of one image; each wave covers a 16*RB-pixel segment of its
-// row, so the image, the row and every kernel row's input row are
-// wave-uniform. The input rows the block touches are copied into LDS as they
-// are (rows of IW*IC bytes, 16-byte loads). Lane l supplies the pixel
-// operand of pixel l & 15 of a row block, K slice l >> 4 = taps 4s .. 4s + 3:
-// each tap is the four bytes at the pixel's input position (two aligned LDS
-// words and a byte shift); the bytes past the channel count land on zero
-// weights, and padding positions use the zero-point word. The channels are
-// the MFMA's rows, so the requantised bytes leave straight from registers
-// (conv_store_direct).
-template <int RB, int NT, int EMODE>
+// Stem convolution (few input channels, kh <= 4, kw * IC <= 16, no column
+// dilation). The K step is one kernel row per 16-lane group: lane group lg
+// holds kernel row ky = lg, and its 16-byte K slice is the kw * IC
+// contiguous input bytes that row covers (byte kx * IC + c; weights are zero
+// past kw * IC and for lane groups past kh). A block is four waves on four
+// consecutive output rows of one image; each wave covers one segment of its
+// row, seg_rb row blocks of 16 pixels, with NRB >= seg_rb row blocks of
+// registers (the rows past the segment are not stored). The input rows the block touches are copied into
+// LDS with a 16-byte gap after each row and 16 bytes before the first; the
+// gaps and the rows outside the image hold the input zero point, so padding
+// columns and rows read as the zero point and every window is one unaligned
+// run of LDS bytes: five aligned words and four byte-aligns per row block, no
+// per-tap bounds test. The channels are the MFMA's rows, so the requantised
+// bytes leave straight from registers (conv_store_direct).
+template <int NT, int NRB, int EMODE>
 __global__ __launch_bounds__(256) void k_conv_stem(ConvArgs a)
 {
-    constexpr int R = RB * 16;
+    constexpr int RB = (NRB + 3) & ~3;
     constexpr bool HI = EMODE & 1, CORR = EMODE & 2;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     __shared__ __attribute__((aligned(4))) int8_t lut_s[256];
     __shared__ int4 epi_s[2 * NT * 16];
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lr = lane & 15, lg = lane >> 4;
     // blockIdx.x = (image * row_groups + row_group) * segments + segment
     const int seg = blockIdx.x % a.segs;
     const int rg = blockIdx.x / a.segs;
     const int n = rg / a.row_groups, oy0 = (rg - n * a.row_groups) * 4, oy = oy0 + wave;
     const bool row_ok = oy < a.oh;
-    const int ox0 = seg * R;
+    const int ox0 = seg * a.seg_rb * 16;
     const int n0 = blockIdx.y * NT * 16;
     const int xzw = (a.xz & 0xff) * 0x01010101;
+    const v4i xzv = {xzw, xzw, xzw, xzw};
     const int rowbytes = a.iw * a.ic;                  // a multiple of 16 (host checked)
-    const int gend = a.ih * rowbytes;                  // image bytes (< 2^31, host checked)
+    const int rs = rowbytes + 16;                      // LDS row stride: the row and its gap
     const int iy_base = oy0 * a.sh - a.pt;             // input row of staged row 0
-    const int8_t *xim = a.x + (long)n * gend;
+    const int8_t *xim = a.x + (long)n * a.ih * rowbytes;
 
-    const int8_t *wrow = a.w + (long)(n0 + lr) * a.kpad + lg * 16;
+    const int8_t *wrow = a.w + (long)(n0 + lr) * 64 + lg * 16;
     v4i B[NT];
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) B[nt] = *(const v4i *)(wrow + (long)nt * 16 * a.kpad);
+    for (int nt = 0; nt < NT; nt++) B[nt] = *(const v4i *)(wrow + (long)nt * 16 * 64);
 
-    // Stage the rows: they are contiguous in the image and in LDS, so chunk c
-    // is image byte iy_base * rowbytes + 16 c. Chunks of rows outside the
-    // image are skipped (never read). Four loads per thread are issued before
-    // the first LDS write.
+    // Stage: chunk c = r * cpr + j is 16-byte piece j of staged row r (the
+    // last piece of a row is its gap), at LDS byte 16 + r * rs + 16 j. Four
+    // loads per thread are in flight before the first LDS write.
     {
-        const int total = a.stem_rows * (rowbytes >> 4), g0 = iy_base * rowbytes;
+        const int cpr = a.stem_cpr, total = a.stem_rows * cpr;
         for (int c0 = threadIdx.x; c0 < total; c0 += 4 * 256) {
             v4i v[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const int c = c0 + j * 256, g = g0 + c * 16;
-                if (c < total && g >= 0 && g < gend) v[j] = *(const v4i *)(xim + g);
+                const int c = c0 + j * 256;
+                const int r = (int)udiv((unsigned)c, (unsigned)cpr, a.stem_cpr_magic), k = c - r * cpr;
+                const int iy = iy_base + r;
+                v[j] = xzv;
+                if (c < total && k < cpr - 1 && (unsigned)iy < (unsigned)a.ih)
+                    v[j] = *(const v4i *)(xim + (long)iy * rowbytes + k * 16);
             }
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const int c = c0 + j * 256, g = g0 + c * 16;
-                if (c < total && g >= 0 && g < gend) ((v4i *)smem)[c] = v[j];
+                const int c = c0 + j * 256;
+                if (c < total) ((v4i *)smem)[1 + c] = v[j];
             }
         }
+        if (threadIdx.x == 0) ((v4i *)smem)[0] = xzv;
     }
     stage_consts<NT>(a, n0, epi_s, lut_s);
 
-    // This lane's four taps: (ky, kx) of tap t = 4 * lg + j by a multiply-shift
-    // ((t * ceil(2^16 / kw)) >> 16 == t / kw for t, kw <= 16).
-    int ry[4], dx[4];
-    bool tap_ok[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int t = lg * 4 + j;
-        const int ky = (t * a.kw_magic) >> 16, kx = t - ky * a.kw;
-        const int iy = oy * a.sh - a.pt + ky * a.dh;
-        tap_ok[j] = t < a.taps && row_ok && (unsigned)iy < (unsigned)a.ih;
-        ry[j] = (iy - iy_base) * rowbytes;
-        dx[j] = kx * a.dw - a.pl;
-    }
+    // Staged row of this lane's kernel row (row 0 for lane groups past kh,
+    // whose weights are zero) and the LDS byte of its window at pixel 0.
+    const int ky = lg < a.kh ? lg : 0;
+    const int wbase = 16 + (wave * a.sh + ky * a.dh) * rs - a.pl * a.ic;
+    const int step = a.sw * a.ic;                      // window bytes between neighbouring pixels
     __syncthreads();
-    const int *lw = (const int *)smem;
-    v4i A[RB];
+    v4i A[NRB];
 #pragma unroll
-    for (int rb = 0; rb < RB; rb++) {
-        const int ox = ox0 + rb * 16 + lr;
-        // Branch-free: every lane reads (offset 0 for padding taps) and
-        // selects afterwards, so all the wave's LDS reads are in flight at
-        // once instead of one round trip per tap.
-        int words[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int ix = ox * a.sw + dx[j];
-            const bool ok = tap_ok[j] && ox < a.ow && (unsigned)ix < (unsigned)a.iw;
-            const int off = ok ? ry[j] + ix * a.ic : 0;
-            const int lo = lw[off >> 2], hi = lw[(off >> 2) + 1];
-            const int v = (int)__builtin_amdgcn_alignbyte((unsigned)hi, (unsigned)lo, (unsigned)(off & 3));
-            words[j] = ok ? v : xzw;
-        }
-        A[rb] = (v4i){words[0], words[1], words[2], words[3]};
+    for (int rb = 0; rb < NRB; rb++) {
+        const int ox = min(ox0 + rb * 16 + lr, a.ow - 1);
+        const int off = wbase + __mul24(ox, step);
+        const int *p = (const int *)(smem + (off & ~3));
+        const int w0 = p[0], w1 = p[1], w2 = p[2], w3 = p[3], w4 = p[4];
+        const unsigned sh = (unsigned)off;             // byte-align uses the low two bits
+        A[rb] = (v4i){(int)__builtin_amdgcn_alignbyte((unsigned)w1, (unsigned)w0, sh),
+                      (int)__builtin_amdgcn_alignbyte((unsigned)w2, (unsigned)w1, sh),
+                      (int)__builtin_amdgcn_alignbyte((unsigned)w3, (unsigned)w2, sh),
+                      (int)__builtin_amdgcn_alignbyte((unsigned)w4, (unsigned)w3, sh)};
     }
     // Channels as the MFMA rows (weights in A), pixels as its columns.
     v4i acc[RB][NT];
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++)
+    for (int rb = 0; rb < NRB; rb++)
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++)
+        for (int nt = 0; nt < NT; nt++)
             acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(B[nt], A[rb], (v4i){0, 0, 0, 0}, 0, 0, 0);
-    // Output pixels of this wave: its output row, ox0 .. min(ox0 + R, ow).
+    // Output pixels of this wave: its output row, ox0 .. min(ox0 + seg_rb * 16, ow).
     const long rbase = ((long)n * a.oh + oy) * a.ow + ox0;
-    const long rlimit = row_ok ? ((long)n * a.oh + oy) * a.ow + a.ow : rbase;
-    conv_store_direct<RB, NT, HI, CORR>(a, acc, n0, lane, rbase, rlimit, epi_s, lut_s);
+    const int send = min(ox0 + a.seg_rb * 16, a.ow);
+    const long rlimit = row_ok ? ((long)n * a.oh + oy) * a.ow + send : rbase;
+    conv_store_direct<RB, NT, HI, CORR, NRB>(a, acc, n0, lane, rbase, rlimit, epi_s, lut_s);
 }
 
-// Dynamic LDS of k_conv_stem (staged input rows plus 16 bytes of slack for
-// the second word of the last tap), 0 when the layer does not fit it: the
-// rows must be a multiple of 16 bytes, the staged rows at most 48 KiB, and OC
-// a multiple of 16 (whole 16-byte stores).
+// Dynamic LDS of k_conv_stem (a 16-byte lead, the staged rows each followed
+// by a 16-byte gap, 32 bytes of slack for the last window's word reads), 0
+// when the layer does not fit it: kh <= 4, no column dilation, kw * IC <= 16,
+// left padding and the columns past the right edge each within 16 bytes,
+// rows a multiple of 16 bytes, the stage at most 48 KiB, and OC a multiple
+// of 16 (whole 16-byte stores).
 static size_t stem_lds(const UQKSpatial *d)
 {
     const int rowbytes = d->iw * d->ic;
     const int rows = 3 * d->sh + (d->kh - 1) * d->dh + 1;
-    const size_t bytes = (size_t)rows * rowbytes + 16;
-    return rowbytes % 16 == 0 && d->oc % 16 == 0 && bytes <= 49152 ? bytes : 0;
+    const int over = (d->ow - 1) * d->sw - d->pl + d->kw - d->iw;
+    const size_t bytes = 16 + (size_t)rows * (rowbytes + 16) + 32;
+    const bool fits = d->kh >= 1 && d->kh <= 4 && d->dw == 1 && d->kw * d->ic <= 16 && d->pl >= 0 &&
+                      d->pl * d->ic <= 16 && (over > 0 ? over : 0) * d->ic <= 16 && rowbytes % 16 == 0 &&
+                      d->oc % 16 == 0 && d->ow >= 1;
+    return fits && bytes <= 49152 ? bytes : 0;
 }
 
 extern "C" int uqk_conv_stem_ok(const UQKSpatial *d) { return stem_lds(d) > 0; }
@@ -1129,33 +1129,51 @@ static int conv_launch(const UQKSpatial *d, const void *x, void *y, uint32_t bat
     if (a.M <= 0) return 0;
     const int nchunks = d->oc_pad / (16 * d->nt);
     if (d->mode == UQK_STEM) {
-        // A block is four output rows x one 128-pixel segment per wave
-        // (eight row blocks: rows up to 128 pixels are one segment, so each
-        // input row is staged once); the channel slice covers up to 64
-        // channels (NT = oc_pad / 16 when that is 1, 2 or 4).
+        // A block is four output rows; each wave covers one segment of its
+        // row, at most eight row blocks of 16 pixels (rows up to 128 pixels
+        // are one segment, so each input row is staged once, and the
+        // segments of longer rows share the row blocks evenly). The channel
+        // slice covers up to 64 channels (NT = oc_pad / 16 when that is 1, 2
+        // or 4).
         const int nt = d->oc_pad == 16 ? 1 : d->oc_pad == 32 ? 2 : 4;
+        const int rbs = (d->ow + 15) / 16;
         a.images = (int)batches;
-        a.segs = (d->ow + 127) / 128;
+        a.segs = (rbs + 7) / 8;
+        a.seg_rb = (rbs + a.segs - 1) / a.segs;
         a.row_groups = (d->oh + 3) / 4;
-        a.kw_magic = (65536 + d->kw - 1) / d->kw;
         a.stem_rows = 3 * d->sh + (d->kh - 1) * d->dh + 1;
+        a.stem_cpr = d->iw * d->ic / 16 + 1;
+        a.stem_cpr_magic = udiv_magic((unsigned)a.stem_cpr);
         const size_t lds = stem_lds(d);
         const unsigned long long items = (unsigned long long)batches * a.row_groups * a.segs;
         if (!lds || items > 0x7fffffffULL || (unsigned long long)d->ih * d->iw * d->ic > 0x7fffffffULL)
             return (int)hipErrorInvalidValue;
         dim3 grid((unsigned)items, (unsigned)(d->oc_pad / (16 * nt)));
-#define UQK_STEM_EM(NT)                                                                                    \
+        // Row blocks of registers per wave: seg_rb, at least four.
+        const int nrb = a.seg_rb < 4 ? 4 : a.seg_rb;
+#define UQK_STEM_EM(NT, NRB)                                                                               \
     do {                                                                                                   \
         switch (a.emode) {                                                                                 \
-        case 0: hipLaunchKernelGGL((k_conv_stem<8, NT, 0>), grid, dim3(256), lds, g_stream, a); break;     \
-        case 1: hipLaunchKernelGGL((k_conv_stem<8, NT, 1>), grid, dim3(256), lds, g_stream, a); break;     \
-        case 2: hipLaunchKernelGGL((k_conv_stem<8, NT, 2>), grid, dim3(256), lds, g_stream, a); break;     \
-        default: hipLaunchKernelGGL((k_conv_stem<8, NT, 3>), grid, dim3(256), lds, g_stream, a); break;    \
+        case 0: hipLaunchKernelGGL((k_conv_stem<NT, NRB, 0>), grid, dim3(256), lds, g_stream, a); break;   \
+        case 1: hipLaunchKernelGGL((k_conv_stem<NT, NRB, 1>), grid, dim3(256), lds, g_stream, a); break;   \
+        case 2: hipLaunchKernelGGL((k_conv_stem<NT, NRB, 2>), grid, dim3(256), lds, g_stream, a); break;   \
+        default: hipLaunchKernelGGL((k_conv_stem<NT, NRB, 3>), grid, dim3(256), lds, g_stream, a); break;  \
         }                                                                                                  \
     } while (0)
-        if (nt == 1) UQK_STEM_EM(1);
-        else if (nt == 2) UQK_STEM_EM(2);
-        else UQK_STEM_EM(4);
+#define UQK_STEM_RB(NT)                                                                                    \
+    do {                                                                                                   \
+        switch (nrb) {                                                                                     \
+        case 4: UQK_STEM_EM(NT, 4); break;                                                                 \
+        case 5: UQK_STEM_EM(NT, 5); break;                                                                 \
+        case 6: UQK_STEM_EM(NT, 6); break;                                                                 \
+        case 7: UQK_STEM_EM(NT, 7); break;                                                                 \
+        default: UQK_STEM_EM(NT, 8); break;                                                                \
+        }                                                                                                  \
+    } while (0)
+        if (nt == 1) UQK_STEM_RB(1);
+        else if (nt == 2) UQK_STEM_RB(2);
+        else UQK_STEM_RB(4);
+#undef UQK_STEM_RB
 #undef UQK_STEM_EM
         UQK_LAUNCHED();
         return 0;
@@ -2779,17 +2797,49 @@ extern "C" int uqk_init(void)
     UQK_TRY(hipGetDeviceCount(&n));
     if (n < 1) return (int)hipErrorNoDevice;
     // All streams at the default priority.
-    UQK_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+    UQK_TRY(hipStreamCreateWithFlags(&g_main, hipStreamNonBlocking));
+    g_stream = g_main;
     UQK_TRY(hipStreamCreateWithFlags(&g_copy[0], hipStreamNonBlocking));
     UQK_TRY(hipStreamCreateWithFlags(&g_copy[1], hipStreamNonBlocking));
     for (int i = 0; i < 8; i++) UQK_TRY(hipEventCreateWithFlags(&g_pipe_ev[i], hipEventDisableTiming));
+    for (int i = 0; i < UQK_MAX_SLICES - 1; i++) {
+        UQK_TRY(hipStreamCreateWithFlags(&g_side[i], hipStreamNonBlocking));
+        UQK_TRY(hipEventCreateWithFlags(&g_join[i], hipEventDisableTiming));
+    }
+    UQK_TRY(hipEventCreateWithFlags(&g_fork, hipEventDisableTiming));
     g_ready = 1;
+    return 0;
+}
+
+// A batch split into image slices, one compute stream each: slice 0 on the
+// main stream, slice k on side stream k - 1. The side streams start after
+// everything already queued on the main stream; split_end makes the main
+// stream wait for all of them, so later work (and uqk_sync) sees the whole
+// batch.
+extern "C" int uqk_split_begin(int slices)
+{
+    if (slices < 1 || slices > UQK_MAX_SLICES) return (int)hipErrorInvalidValue;
+    UQK_TRY(hipEventRecord(g_fork, g_main));
+    for (int k = 0; k < slices - 1; k++) UQK_TRY(hipStreamWaitEvent(g_side[k], g_fork, 0));
+    return 0;
+}
+
+extern "C" void uqk_split_use(int slice) { g_stream = slice > 0 ? g_side[slice - 1] : g_main; }
+
+extern "C" int uqk_split_end(int slices)
+{
+    g_stream = g_main;
+    if (slices < 1 || slices > UQK_MAX_SLICES) return (int)hipErrorInvalidValue;
+    for (int k = 0; k < slices - 1; k++) {
+        UQK_TRY(hipEventRecord(g_join[k], g_side[k]));
+        UQK_TRY(hipStreamWaitEvent(g_main, g_join[k], 0));
+    }
     return 0;
 }
 
 // Stream ids for the pipelined transfers: 0 compute, 1 host-to-device,
 // 2 device-to-host.
-static hipStream_t stream_of(int id) { return id == 0 ? g_stream : g_copy[id - 1]; }
+static hipStream_t stream_of(int id) { return id == 0 ? g_main : g_copy[id - 1]; }
 
 extern "C" int uqk_copy_on(int stream, void *dst, const void *src, size_t bytes, int to_device)
 {
@@ -2816,7 +2866,7 @@ extern "C" int uqk_pipe_wait(int stream, int event)
 extern "C" int uqk_sync_all(void)
 {
     UQK_TRY(hipStreamSynchronize(g_copy[0]));
-    UQK_TRY(hipStreamSynchronize(g_stream));
+    UQK_TRY(hipStreamSynchronize(g_main));
     UQK_TRY(hipStreamSynchronize(g_copy[1]));
     return 0;
 }

@@ -39,8 +39,8 @@ typedef struct {
 /* Conv A-operand sources: pointwise rows, per-lane gathers with 16/4/1-byte
  * granularity, LDS-staged input rows (16-byte slices, or 4-byte words over
  * channels padded to a multiple of four), or the stem form (at most four
- * input channels and 16 taps: every tap is one 4-byte word read straight
- * from the input and the receptive field is one 64-byte K step). */
+ * kernel rows of kw * IC <= 16 contiguous input bytes each: the receptive
+ * field is one 64-byte K step, 16 bytes per kernel row). */
 enum { UQK_PW = 0, UQK_G16 = 1, UQK_G4 = 2, UQK_G1 = 3, UQK_ROWS16 = 4, UQK_ROWS4 = 5, UQK_STEM = 6 };
 
 /* Dynamic LDS bytes of the tap-window depthwise kernel for a layer, 0 when
@@ -69,8 +69,10 @@ typedef struct {
 size_t uqk_ib_lds(int P, int Cin, int Ce, int Cout, int ks, size_t *offsets);
 int uqk_ib(const UQKIb *f, const void *x, void *y, uint32_t images);
 
-/* Whether a conv layer fits the stem kernel (input rows a multiple of 16
- * bytes, its staged rows within 48 KiB, OC % 16 == 0). */
+/* Whether a conv layer fits the stem kernel (kh <= 4, kw * IC <= 16, no
+ * column dilation, left and right padding within 16 bytes, input rows a
+ * multiple of 16 bytes, its staged rows within 48 KiB, OC % 16 == 0). Reads
+ * iw, ic, kh, kw, sh, sw, dh, dw, pl, ow and oc. */
 int uqk_conv_stem_ok(const UQKSpatial *d);
 
 /* Dynamic LDS bytes k_conv_rows needs for a layer at rb row blocks per wave. */
@@ -98,6 +100,18 @@ int uqk_copy_on(int stream, void *dst, const void *src, size_t bytes, int to_dev
 int uqk_pipe_record(int event, int stream);
 int uqk_pipe_wait(int stream, int event);
 int uqk_sync_all(void);
+
+/* Image slices of one batch on separate compute streams (at most
+ * UQK_MAX_SLICES): split_begin orders the side streams after the main
+ * stream's queued work, split_use(k) sends the following launches to slice
+ * k's stream, split_end joins the side streams into the main stream and
+ * makes it current again. Two: the main stream, the two transfer streams
+ * and one side stream are HIP's default four hardware queues (more streams
+ * would share a queue, and more queues measured far slower). */
+#define UQK_MAX_SLICES 2
+int uqk_split_begin(int slices);
+void uqk_split_use(int slice);
+int uqk_split_end(int slices);
 void *uqk_host_alloc(size_t bytes);                   /* pinned (hipHostMalloc) */
 void uqk_host_free(void *p);
 
