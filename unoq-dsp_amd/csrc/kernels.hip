@@ -25,6 +25,7 @@ static hipStream_t g_copy[2];     // host transfers of the pipelined batch: in, 
 static hipEvent_t g_pipe_ev[8];   // pipeline hand-offs between the three streams
 static hipStream_t g_side[UQK_MAX_SLICES - 1];   // compute streams of the other image slices
 static hipEvent_t g_fork, g_join[UQK_MAX_SLICES - 1];
+static int g_live_slices = 1;     // launches in flight side by side (image slices of one batch)
 static int g_ready;
 static int g_err;
 static hipEvent_t *g_events;
@@ -1201,14 +1202,16 @@ static int conv_launch(const UQKSpatial *d, const void *x, void *y, uint32_t bat
         // Narrower channel slices when the batch gives too few waves to keep
         // four per SIMD (1024 SIMDs): more slices re-read the (small) input
         // but hide the K loop's load latency. 8 -> 4 -> 2 and 6 -> 2 keep
-        // oc_pad (a multiple of 16 * NT) a whole number of slices.
+        // oc_pad (a multiple of 16 * NT) a whole number of slices. The rows
+        // of the image slices running side by side count together.
         int nt = d->nt;
-        const long row_waves = (a.M + 15) / 16;
+        const long m_live = a.M * g_live_slices;
+        const long row_waves = (m_live + 15) / 16;
         while (nt > 2 && row_waves * (d->oc_pad / (16 * nt)) < 4096) nt = nt == 8 ? 4 : 2;
         const int chunks = d->oc_pad / (16 * nt);
         // Two row blocks per wave only when that still gives every SIMD of
         // the chip several waves.
-        const long waves2 = (a.M + 31) / 32 * chunks;
+        const long waves2 = (m_live + 31) / 32 * chunks;
         const int rb = waves2 >= 8192 ? 2 : 1;
         const long rows = 4L * 16 * rb;
         dim3 grid((unsigned)((a.M + rows - 1) / rows), (unsigned)chunks);
@@ -2819,6 +2822,7 @@ extern "C" int uqk_init(void)
 extern "C" int uqk_split_begin(int slices)
 {
     if (slices < 1 || slices > UQK_MAX_SLICES) return (int)hipErrorInvalidValue;
+    g_live_slices = slices;
     UQK_TRY(hipEventRecord(g_fork, g_main));
     for (int k = 0; k < slices - 1; k++) UQK_TRY(hipStreamWaitEvent(g_side[k], g_fork, 0));
     return 0;
@@ -2829,6 +2833,7 @@ extern "C" void uqk_split_use(int slice) { g_stream = slice > 0 ? g_side[slice -
 extern "C" int uqk_split_end(int slices)
 {
     g_stream = g_main;
+    g_live_slices = 1;
     if (slices < 1 || slices > UQK_MAX_SLICES) return (int)hipErrorInvalidValue;
     for (int k = 0; k < slices - 1; k++) {
         UQK_TRY(hipEventRecord(g_join[k], g_side[k]));
