@@ -58,7 +58,9 @@ def time_device(lib, graph, images, steps, warmup, seed=7):
         assert rc == 0, rc
     assert lib.ug_synchronize() == 0
     seconds = time.perf_counter() - t0
-    # Per-op HIP-event durations over the same number of steps.
+    # Per-op durations from HIP events stamped by the kernels' own dispatches
+    # (first start to last end of each op's kernels), over the same number
+    # of steps.
     graph.profile(1)
     for _ in range(steps):
         rc = lib.ug_run_device(din.ptr, dout.ptr, images)

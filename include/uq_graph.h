@@ -53,7 +53,8 @@ int ug_snapshot(uint32_t tensor, void *out, uint32_t bytes);
 
 /* graph.h:45, graph.c:269-284. command 0 disable, 1 reset+enable, 2 read.
  * Counters: [0] runs, [1] total ticks, [2+i] ticks of op i. Ticks are GPU
- * nanoseconds from HIP events on the library stream. bytes = 514*8, or 130*8
+ * nanoseconds from the first start to the last end of an op's kernels (HIP
+ * events stamped by the launches themselves). bytes = 514*8, or 130*8
  * when the plan has at most 128 ops. */
 int ug_profile(uint32_t command, void *out, uint32_t bytes);
 

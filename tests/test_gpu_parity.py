@@ -163,6 +163,26 @@ def test_profile_counters(lib):
     assert c[0] == 3 and c[1] > 0 and c[2] > 0
 
 
+@pytest.mark.parametrize("name", ["mnv4", "yolo"])
+def test_profiled_run_keeps_bytes(lib, name):
+    """A profiled run (every op alone on the stream, its kernels stamping the
+    op's events) gives the unprofiled bytes, and every op that launches work
+    gets ticks no larger than the run's total."""
+    plan, _ = W.WORKLOADS[name]()
+    images = 3
+    x = P.random_input(plan, images, 8)
+    g = Graph(plan, lib)
+    want = g.run_batch(x, images)
+    g.profile(1)
+    _assert_same(g.run_batch(x, images), want, f"{name} profiled")
+    c = g.profile(2)
+    g.profile(0)
+    kinds = [o[0] for o in P.op_records(plan)]
+    ticks = c[2:2 + len(kinds)]
+    assert c[0] == 1 and c[1] == ticks.sum()
+    assert all(ticks[i] > 0 for i, k in enumerate(kinds) if k != 5)
+
+
 def test_bad_sizes_rejected(lib):
     plan, _ = W.pointwise()
     g = Graph(plan, lib)

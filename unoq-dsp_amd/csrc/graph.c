@@ -929,7 +929,7 @@ static int prepare_device(void)
     if (!rc) rc = uqk_h2d(G.dev_prep, host_pool, at + 256);
     if (!rc) rc = uqk_sync();
     free(host_pool);
-    if (!rc) rc = uqk_events(G.h.no + 1);
+    if (!rc) rc = uqk_events(G.h.no);
     return rc ? 24 : 0;
 }
 
@@ -1062,9 +1062,7 @@ static int enqueue_ops(uint32_t images)
     int rc = 0;
     uint32_t next = 0;
     if (n == 1) {
-        rc = enqueue_range(0, G.h.no, images, &next);
-        if (!rc && G.profile_enabled) rc = uqk_record(G.h.no);
-        return rc;
+        return enqueue_range(0, G.h.no, images, &next);
     }
     static uint8_t *tab[UQK_MAX_SLICES][UG_MAX_T];
     uint32_t first[UQK_MAX_SLICES + 1];
@@ -1093,7 +1091,20 @@ static int enqueue_ops(uint32_t images)
     return rc;
 }
 
+static int launch_op(uint32_t i, uint32_t images);
+
+/* Enqueue op i; while profiling, with its kernels stamping the op's timing
+ * events. */
 static int enqueue_op(uint32_t i, uint32_t images)
+{
+    if (!G.profile_enabled) return launch_op(i, images);
+    int rc = uqk_time_begin(i);
+    if (!rc) rc = launch_op(i, images);
+    int rc2 = uqk_time_end(i);
+    return rc ? rc : rc2;
+}
+
+static int launch_op(uint32_t i, uint32_t images)
 {
     const uint8_t *A = G.arena;
     {
@@ -1102,7 +1113,6 @@ static int enqueue_op(uint32_t i, uint32_t images)
         void *zp = G.ptr[o->out];
         const void *ap = G.ptr[o->a], *bp = G.ptr[o->b];
         int rc = 0;
-        if (G.profile_enabled && (rc = uqk_record(i))) return rc;
         switch (o->code) {
         case 14: rc = uqk_conv(G.sp + i, ap, zp, images * a->d[0]); break;
         case 15: rc = uqk_depthwise(G.sp + i, ap, zp, images * a->d[0]); break;
@@ -1240,7 +1250,7 @@ static int finish_profile(void)
     uint64_t total = 0;
     for (uint32_t i = 0; i < G.h.no; i++) {
         uint64_t ns = 0;
-        if (uqk_elapsed_ns(i, i + 1, &ns)) return 24;
+        if (uqk_op_ns(i, &ns)) return 24;
         G.ticks[2 + i] += ns;
         total += ns;
     }

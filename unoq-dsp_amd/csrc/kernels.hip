@@ -13,6 +13,7 @@
 //   * depthwise (code 15) and pooling (code 16) are bandwidth kernels on the
 //     vector ALU; add/mean/LUT/resize/pad/slice are byte-movement kernels.
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <type_traits>
 #include <stdint.h>
 #include "uqk.h"
@@ -28,8 +29,10 @@ static hipEvent_t g_fork, g_join[UQK_MAX_SLICES - 1];
 static int g_live_slices = 1;     // launches in flight side by side (image slices of one batch)
 static int g_ready;
 static int g_err;
-static hipEvent_t *g_events;
+static hipEvent_t *g_ev_start, *g_ev_stop;   // per-op timing events (profiling)
 static uint32_t g_nevents;
+static int g_timing;              // an op is being timed: its launches stamp its events
+static uint32_t g_timed_op, g_timed_launches;
 
 #define UQK_TRY(expr)                                  \
     do {                                               \
@@ -40,6 +43,24 @@ static uint32_t g_nevents;
         }                                              \
     } while (0)
 #define UQK_LAUNCHED() UQK_TRY(hipGetLastError())
+
+// Every kernel launch goes to g_stream. While an op is timed (uqk_time_begin
+// .. uqk_time_end), its first launch stamps the op's start event and every
+// launch its stop event with the dispatch's own start and end timestamps (the
+// interval a kernel trace reports, without the gap an event record between
+// kernels adds). The stream argument of the call sites is g_stream.
+template <typename F, typename... Args>
+static inline void uqk_launch(F kernel, dim3 grid, dim3 block, size_t lds, Args... args)
+{
+    hipEvent_t start = nullptr, stop = nullptr;
+    if (g_timing) {
+        start = g_timed_launches ? nullptr : g_ev_start[g_timed_op];
+        stop = g_ev_stop[g_timed_op];
+        g_timed_launches++;
+    }
+    hipExtLaunchKernelGGL(kernel, grid, block, (std::uint32_t)lds, g_stream, start, stop, 0u, args...);
+}
+#define UQK_LAUNCH(kernel, grid, block, lds, stream, ...) uqk_launch(kernel, grid, block, lds, __VA_ARGS__)
 
 // ---------------------------------------------------------------------------
 // Requantisation: qnn.c:61-83 followed by the zero point and clamp.
@@ -995,19 +1016,19 @@ static void launch_conv_mode(int mode, const ConvArgs &a, dim3 grid, size_t)
 #define UQK_PW_EM(ADD)                                                                                          \
     do {                                                                                                        \
         switch (a.emode) {                                                                                      \
-        case 0: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 0, ADD>), grid, dim3(256), lds, g_stream, a); break;  \
-        case 1: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 1, ADD>), grid, dim3(256), lds, g_stream, a); break;  \
-        case 2: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 2, ADD>), grid, dim3(256), lds, g_stream, a); break;  \
-        default: hipLaunchKernelGGL((k_conv<RB, NT, UQK_PW, 3, ADD>), grid, dim3(256), lds, g_stream, a); break; \
+        case 0: UQK_LAUNCH((k_conv<RB, NT, UQK_PW, 0, ADD>), grid, dim3(256), lds, g_stream, a); break;  \
+        case 1: UQK_LAUNCH((k_conv<RB, NT, UQK_PW, 1, ADD>), grid, dim3(256), lds, g_stream, a); break;  \
+        case 2: UQK_LAUNCH((k_conv<RB, NT, UQK_PW, 2, ADD>), grid, dim3(256), lds, g_stream, a); break;  \
+        default: UQK_LAUNCH((k_conv<RB, NT, UQK_PW, 3, ADD>), grid, dim3(256), lds, g_stream, a); break; \
         }                                                                                                       \
     } while (0)
         if (a.res) UQK_PW_EM(true);
         else UQK_PW_EM(false);
 #undef UQK_PW_EM
         break;
-    case UQK_G16: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G16, -1, true>), grid, dim3(256), lds, g_stream, a); break;
-    case UQK_G4: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G4, -1, true>), grid, dim3(256), lds, g_stream, a); break;
-    default: hipLaunchKernelGGL((k_conv<RB, NT, UQK_G1, -1, true>), grid, dim3(256), lds, g_stream, a); break;
+    case UQK_G16: UQK_LAUNCH((k_conv<RB, NT, UQK_G16, -1, true>), grid, dim3(256), lds, g_stream, a); break;
+    case UQK_G4: UQK_LAUNCH((k_conv<RB, NT, UQK_G4, -1, true>), grid, dim3(256), lds, g_stream, a); break;
+    default: UQK_LAUNCH((k_conv<RB, NT, UQK_G1, -1, true>), grid, dim3(256), lds, g_stream, a); break;
     }
 }
 
@@ -1031,10 +1052,10 @@ static void launch_rows_nt(int nt, int mode, const ConvArgs &a, dim3 grid, size_
 #define UQK_ROWS_EM(NT, W)                                                                                      \
     do {                                                                                                        \
         switch (a.emode) {                                                                                      \
-        case 0: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 0, DIR>), grid, dim3(256), lds, g_stream, a); break; \
-        case 1: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 1, DIR>), grid, dim3(256), lds, g_stream, a); break; \
-        case 2: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 2, DIR>), grid, dim3(256), lds, g_stream, a); break; \
-        default: hipLaunchKernelGGL((k_conv_rows<RB, NT, W, 3, DIR>), grid, dim3(256), lds, g_stream, a); break; \
+        case 0: UQK_LAUNCH((k_conv_rows<RB, NT, W, 0, DIR>), grid, dim3(256), lds, g_stream, a); break; \
+        case 1: UQK_LAUNCH((k_conv_rows<RB, NT, W, 1, DIR>), grid, dim3(256), lds, g_stream, a); break; \
+        case 2: UQK_LAUNCH((k_conv_rows<RB, NT, W, 2, DIR>), grid, dim3(256), lds, g_stream, a); break; \
+        default: UQK_LAUNCH((k_conv_rows<RB, NT, W, 3, DIR>), grid, dim3(256), lds, g_stream, a); break; \
         }                                                                                                       \
     } while (0)
 #define UQK_ROWS_LAUNCH(NT)                                                                                     \
@@ -1155,10 +1176,10 @@ static int conv_launch(const UQKSpatial *d, const void *x, void *y, uint32_t bat
 #define UQK_STEM_EM(NT, NRB)                                                                               \
     do {                                                                                                   \
         switch (a.emode) {                                                                                 \
-        case 0: hipLaunchKernelGGL((k_conv_stem<NT, NRB, 0>), grid, dim3(256), lds, g_stream, a); break;   \
-        case 1: hipLaunchKernelGGL((k_conv_stem<NT, NRB, 1>), grid, dim3(256), lds, g_stream, a); break;   \
-        case 2: hipLaunchKernelGGL((k_conv_stem<NT, NRB, 2>), grid, dim3(256), lds, g_stream, a); break;   \
-        default: hipLaunchKernelGGL((k_conv_stem<NT, NRB, 3>), grid, dim3(256), lds, g_stream, a); break;  \
+        case 0: UQK_LAUNCH((k_conv_stem<NT, NRB, 0>), grid, dim3(256), lds, g_stream, a); break;   \
+        case 1: UQK_LAUNCH((k_conv_stem<NT, NRB, 1>), grid, dim3(256), lds, g_stream, a); break;   \
+        case 2: UQK_LAUNCH((k_conv_stem<NT, NRB, 2>), grid, dim3(256), lds, g_stream, a); break;   \
+        default: UQK_LAUNCH((k_conv_stem<NT, NRB, 3>), grid, dim3(256), lds, g_stream, a); break;  \
         }                                                                                                  \
     } while (0)
 #define UQK_STEM_RB(NT)                                                                                    \
@@ -1666,10 +1687,10 @@ static int launch_dw_win(const UQKSpatial *d, const void *x, void *y, uint32_t b
 #define UQK_DWW(K, S)                                                                                        \
     do {                                                                                                     \
         switch (mode) {                                                                                      \
-        case 0: hipLaunchKernelGGL((k_dw_win<K, S, false, false>), grid, dim3(256), lds, g_stream, a); break; \
-        case 1: hipLaunchKernelGGL((k_dw_win<K, S, true, false>), grid, dim3(256), lds, g_stream, a); break;  \
-        case 2: hipLaunchKernelGGL((k_dw_win<K, S, false, true>), grid, dim3(256), lds, g_stream, a); break;  \
-        default: hipLaunchKernelGGL((k_dw_win<K, S, true, true>), grid, dim3(256), lds, g_stream, a); break;  \
+        case 0: UQK_LAUNCH((k_dw_win<K, S, false, false>), grid, dim3(256), lds, g_stream, a); break; \
+        case 1: UQK_LAUNCH((k_dw_win<K, S, true, false>), grid, dim3(256), lds, g_stream, a); break;  \
+        case 2: UQK_LAUNCH((k_dw_win<K, S, false, true>), grid, dim3(256), lds, g_stream, a); break;  \
+        default: UQK_LAUNCH((k_dw_win<K, S, true, true>), grid, dim3(256), lds, g_stream, a); break;  \
         }                                                                                                    \
     } while (0)
     if (d->kh == 3 && d->sh == 1) UQK_DWW(3, 1);
@@ -1859,10 +1880,10 @@ static int launch_dw_mfma(const UQKSpatial *d, const void *x, void *y, uint32_t 
 #define UQK_DWM(K, S)                                                                                           \
     do {                                                                                                        \
         switch (mode) {                                                                                         \
-        case 0: hipLaunchKernelGGL((k_dw_mfma<K, S, false, false>), dim3((unsigned)blocks), dim3(256), lds, g_stream, a); break; \
-        case 1: hipLaunchKernelGGL((k_dw_mfma<K, S, true, false>), dim3((unsigned)blocks), dim3(256), lds, g_stream, a); break;  \
-        case 2: hipLaunchKernelGGL((k_dw_mfma<K, S, false, true>), dim3((unsigned)blocks), dim3(256), lds, g_stream, a); break;  \
-        default: hipLaunchKernelGGL((k_dw_mfma<K, S, true, true>), dim3((unsigned)blocks), dim3(256), lds, g_stream, a); break;  \
+        case 0: UQK_LAUNCH((k_dw_mfma<K, S, false, false>), dim3((unsigned)blocks), dim3(256), lds, g_stream, a); break; \
+        case 1: UQK_LAUNCH((k_dw_mfma<K, S, true, false>), dim3((unsigned)blocks), dim3(256), lds, g_stream, a); break;  \
+        case 2: UQK_LAUNCH((k_dw_mfma<K, S, false, true>), dim3((unsigned)blocks), dim3(256), lds, g_stream, a); break;  \
+        default: UQK_LAUNCH((k_dw_mfma<K, S, true, true>), dim3((unsigned)blocks), dim3(256), lds, g_stream, a); break;  \
         }                                                                                                       \
     } while (0)
     if (d->kh == 3 && d->sh == 1) UQK_DWM(3, 1);
@@ -2132,8 +2153,8 @@ extern "C" int uqk_ib(const UQKIb *f, const void *x, void *y, uint32_t images)
         else UQK_TRY(hipFuncSetAttribute((const void *)k_ib<5>, hipFuncAttributeMaxDynamicSharedMemorySize, 163840));
         ceiling_set[which] = 1;
     }
-    if (which == 0) hipLaunchKernelGGL(k_ib<3>, dim3(images), dim3(1024), lds, g_stream, a);
-    else hipLaunchKernelGGL(k_ib<5>, dim3(images), dim3(1024), lds, g_stream, a);
+    if (which == 0) UQK_LAUNCH(k_ib<3>, dim3(images), dim3(1024), lds, g_stream, a);
+    else UQK_LAUNCH(k_ib<5>, dim3(images), dim3(1024), lds, g_stream, a);
     UQK_LAUNCHED();
     return 0;
 }
@@ -2175,8 +2196,8 @@ static int launch_dw_tile(const UQKSpatial *d, const void *x, void *y, uint32_t 
     a.xz = d->xz; a.yz = d->yz; a.lo = d->lo; a.hi = d->hi; a.corr = d->corr;
     const int tiles_y = (d->oh + a.th - 1) / a.th;
     dim3 grid((unsigned)(tiles_y * a.tiles_x), (unsigned)(d->oc / (16 * a.cg)), batches);
-    if (d->kh == 3) hipLaunchKernelGGL(k_dw_tile<3>, grid, dim3(256), lds, g_stream, a);
-    else hipLaunchKernelGGL(k_dw_tile<5>, grid, dim3(256), lds, g_stream, a);
+    if (d->kh == 3) UQK_LAUNCH(k_dw_tile<3>, grid, dim3(256), lds, g_stream, a);
+    else UQK_LAUNCH(k_dw_tile<5>, grid, dim3(256), lds, g_stream, a);
     UQK_LAUNCHED();
     return 0;
 }
@@ -2201,7 +2222,7 @@ static int launch_window(const UQKSpatial *d, const void *x, void *y, uint32_t b
     if (a.total <= 0) return 0;
     dim3 grid((unsigned)((a.total + 255) / 256));
     const int ks = d->kh == d->kw && (d->kh == 3 || d->kh == 5) ? d->kh : 0;
-#define UQK_WIN(V, P, K) hipLaunchKernelGGL((k_window<V, P, K>), grid, dim3(256), 0, g_stream, a)
+#define UQK_WIN(V, P, K) UQK_LAUNCH((k_window<V, P, K>), grid, dim3(256), 0, g_stream, a)
 #define UQK_WIN_KS(V, P) do { if (ks == 3) UQK_WIN(V, P, 3); else if (ks == 5) UQK_WIN(V, P, 5); else UQK_WIN(V, P, 0); } while (0)
     if (pool) {
         if (vec == 16) UQK_WIN_KS(16, true);
@@ -2277,7 +2298,7 @@ extern "C" int uqk_add(const void *a, const void *b, void *y, uint64_t count, co
 {
     if (!count) return 0;
     const uint64_t threads = (count + 15) / 16;
-    hipLaunchKernelGGL(k_add, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, g_stream,
+    UQK_LAUNCH(k_add, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, g_stream,
                        (const int8_t *)a, (const int8_t *)b, (int8_t *)y, count, (const int *)tables, m, shift, yz, lo, hi);
     UQK_LAUNCHED();
     return 0;
@@ -2327,14 +2348,14 @@ extern "C" int uqk_mean(const void *x, void *y, uint32_t batches, uint32_t pixel
     if (channels % 4 == 0) {
         const uint64_t total = (uint64_t)batches * (channels / 4);
         if (!total) return 0;
-        hipLaunchKernelGGL(k_mean4, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g_stream,
+        UQK_LAUNCH(k_mean4, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g_stream,
                            (const int8_t *)x, (int8_t *)y, batches, pixels, channels, xz, yz, m, shift);
         UQK_LAUNCHED();
         return 0;
     }
     const uint64_t total = (uint64_t)batches * channels;
     if (!total) return 0;
-    hipLaunchKernelGGL(k_mean, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g_stream,
+    UQK_LAUNCH(k_mean, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g_stream,
                        (const int8_t *)x, (int8_t *)y, batches, pixels, channels, xz, yz, m, shift);
     UQK_LAUNCHED();
     return 0;
@@ -2370,7 +2391,7 @@ extern "C" int uqk_lut(const void *x, void *y, uint64_t count, const void *table
 {
     if (!count) return 0;
     const uint64_t threads = (count + 15) / 16;
-    hipLaunchKernelGGL(k_lut, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, g_stream,
+    UQK_LAUNCH(k_lut, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, g_stream,
                        (const uint8_t *)x, (uint8_t *)y, count, (const uint8_t *)table, flip);
     UQK_LAUNCHED();
     return 0;
@@ -2409,11 +2430,11 @@ extern "C" int uqk_resize(const void *x, void *y, uint32_t batches, uint32_t ih,
     const uint64_t in_stride = (uint64_t)ih * iw * c;
     dim3 grid((unsigned)((total + 255) / 256));
     if (vec == 16)
-        hipLaunchKernelGGL(k_resize<16>, grid, dim3(256), 0, g_stream, (const int8_t *)x, (int8_t *)y, total, groups, oh, ow, c, in_stride, (const uint32_t *)offsets);
+        UQK_LAUNCH(k_resize<16>, grid, dim3(256), 0, g_stream, (const int8_t *)x, (int8_t *)y, total, groups, oh, ow, c, in_stride, (const uint32_t *)offsets);
     else if (vec == 4)
-        hipLaunchKernelGGL(k_resize<4>, grid, dim3(256), 0, g_stream, (const int8_t *)x, (int8_t *)y, total, groups, oh, ow, c, in_stride, (const uint32_t *)offsets);
+        UQK_LAUNCH(k_resize<4>, grid, dim3(256), 0, g_stream, (const int8_t *)x, (int8_t *)y, total, groups, oh, ow, c, in_stride, (const uint32_t *)offsets);
     else
-        hipLaunchKernelGGL(k_resize<1>, grid, dim3(256), 0, g_stream, (const int8_t *)x, (int8_t *)y, total, groups, oh, ow, c, in_stride, (const uint32_t *)offsets);
+        UQK_LAUNCH(k_resize<1>, grid, dim3(256), 0, g_stream, (const int8_t *)x, (int8_t *)y, total, groups, oh, ow, c, in_stride, (const uint32_t *)offsets);
     UQK_LAUNCHED();
     return 0;
 }
@@ -2461,7 +2482,7 @@ extern "C" int uqk_window4(const void *x, void *y, uint32_t images, const uint32
     }
     const uint64_t total = out_bytes * images;
     if (!total) return 0;
-    hipLaunchKernelGGL(k_window4, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g_stream,
+    UQK_LAUNCH(k_window4, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g_stream,
                        (const int8_t *)x, (int8_t *)y, total, g, fill, in_bytes, out_bytes);
     UQK_LAUNCHED();
     return 0;
@@ -2514,9 +2535,9 @@ extern "C" int uqk_rows2(void *y, uint64_t dp, const void *a, uint64_t s1, uint6
     g.total = rows * g.cpr;
     if (g.total >> 32) return (int)hipErrorInvalidValue;
     const dim3 grid((unsigned)((g.total + 255) / 256));
-    if (V == 16) hipLaunchKernelGGL(k_rows2<16>, grid, dim3(256), 0, g_stream, g);
-    else if (V == 4) hipLaunchKernelGGL(k_rows2<4>, grid, dim3(256), 0, g_stream, g);
-    else hipLaunchKernelGGL(k_rows2<1>, grid, dim3(256), 0, g_stream, g);
+    if (V == 16) UQK_LAUNCH(k_rows2<16>, grid, dim3(256), 0, g_stream, g);
+    else if (V == 4) UQK_LAUNCH(k_rows2<4>, grid, dim3(256), 0, g_stream, g);
+    else UQK_LAUNCH(k_rows2<1>, grid, dim3(256), 0, g_stream, g);
     UQK_LAUNCHED();
     return 0;
 }
@@ -2566,9 +2587,9 @@ extern "C" int uqk_permute(const void *x, void *y, uint32_t images, uint32_t ran
     if (!total) return 0;
     dim3 grid((unsigned)((total + 255) / 256));
     if (elem_bytes == 4)
-        hipLaunchKernelGGL(k_permute<uint32_t>, grid, dim3(256), 0, g_stream, (const uint32_t *)x, (uint32_t *)y, total, count, g);
+        UQK_LAUNCH(k_permute<uint32_t>, grid, dim3(256), 0, g_stream, (const uint32_t *)x, (uint32_t *)y, total, count, g);
     else
-        hipLaunchKernelGGL(k_permute<uint8_t>, grid, dim3(256), 0, g_stream, (const uint8_t *)x, (uint8_t *)y, total, count, g);
+        UQK_LAUNCH(k_permute<uint8_t>, grid, dim3(256), 0, g_stream, (const uint8_t *)x, (uint8_t *)y, total, count, g);
     UQK_LAUNCHED();
     return 0;
 }
@@ -2608,7 +2629,7 @@ extern "C" int uqk_mul(const void *a, const void *b, void *y, uint64_t count, co
 {
     if (!count) return 0;
     const uint64_t threads = (count + 15) / 16;
-    hipLaunchKernelGGL(k_mul, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, g_stream,
+    UQK_LAUNCH(k_mul, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, g_stream,
                        (const int8_t *)a, (const int8_t *)b, (int8_t *)y, count, q[0], q[1], q[2], q[3], q[4], q[5], q[6]);
     UQK_LAUNCHED();
     return 0;
@@ -2677,7 +2698,7 @@ extern "C" int uqk_bmm(const void *a, const void *b, void *z, uint32_t images, u
     if (!blocks) return 0;
     if (blocks > 0x7fffffffULL) return (int)hipErrorInvalidValue;
     const uint64_t b_stride = (uint64_t)batches * k * n;
-    hipLaunchKernelGGL(k_bmm, dim3((unsigned)blocks), dim3(256), 0, g_stream, (const int8_t *)a, (const int8_t *)b,
+    UQK_LAUNCH(k_bmm, dim3((unsigned)blocks), dim3(256), 0, g_stream, (const int8_t *)a, (const int8_t *)b,
                        (int8_t *)z, m, n, k, tiles_m, tiles_n, batches, b_stride, q[5], q[6], q[0], q[1], q[2], q[3], q[4]);
     UQK_LAUNCHED();
     return 0;
@@ -2768,7 +2789,7 @@ extern "C" int uqk_softmax_table(const void *x, void *y, uint64_t rows, uint32_t
                                  int32_t hi)
 {
     if (!rows) return 0;
-    hipLaunchKernelGGL(k_softmax_table, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, g_stream, (const int8_t *)x,
+    UQK_LAUNCH(k_softmax_table, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, g_stream, (const int8_t *)x,
                        (int8_t *)y, rows, width, (const int *)table, lo, hi);
     UQK_LAUNCHED();
     return 0;
@@ -2777,7 +2798,7 @@ extern "C" int uqk_softmax_table(const void *x, void *y, uint64_t rows, uint32_t
 extern "C" int uqk_softmax(const void *x, void *y, uint64_t rows, uint32_t width, const void *table)
 {
     if (!rows) return 0;
-    hipLaunchKernelGGL(k_softmax, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, g_stream, (const int8_t *)x,
+    UQK_LAUNCH(k_softmax, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, g_stream, (const int8_t *)x,
                        (int8_t *)y, rows, width, (const int *)table);
     UQK_LAUNCHED();
     return 0;
@@ -2970,28 +2991,46 @@ extern "C" int uqk_last_error(void) { return g_err; }
 extern "C" int uqk_events(uint32_t count)
 {
     if (count <= g_nevents) return 0;
-    hipEvent_t *ev = (hipEvent_t *)realloc(g_events, sizeof(hipEvent_t) * count);
-    if (!ev) return (int)hipErrorOutOfMemory;
-    g_events = ev;
+    hipEvent_t *e0 = (hipEvent_t *)realloc(g_ev_start, sizeof(hipEvent_t) * count);
+    if (!e0) return (int)hipErrorOutOfMemory;
+    g_ev_start = e0;
+    hipEvent_t *e1 = (hipEvent_t *)realloc(g_ev_stop, sizeof(hipEvent_t) * count);
+    if (!e1) return (int)hipErrorOutOfMemory;
+    g_ev_stop = e1;
     for (uint32_t i = g_nevents; i < count; i++) {
-        UQK_TRY(hipEventCreate(&g_events[i]));
+        UQK_TRY(hipEventCreate(&g_ev_start[i]));
+        UQK_TRY(hipEventCreate(&g_ev_stop[i]));
         g_nevents = i + 1;
     }
     return 0;
 }
 
-extern "C" int uqk_record(uint32_t index)
+// Time op `index`: its start event is recorded now on the stream and
+// re-stamped by the op's first kernel; an op that launches no kernel (only
+// copies, or nothing) gets its stop event recorded at uqk_time_end.
+extern "C" int uqk_time_begin(uint32_t index)
 {
     if (index >= g_nevents) return (int)hipErrorInvalidValue;
-    UQK_TRY(hipEventRecord(g_events[index], g_stream));
+    UQK_TRY(hipEventRecord(g_ev_start[index], g_stream));
+    g_timing = 1;
+    g_timed_op = index;
+    g_timed_launches = 0;
     return 0;
 }
 
-extern "C" int uqk_elapsed_ns(uint32_t first, uint32_t second, uint64_t *ns)
+extern "C" int uqk_time_end(uint32_t index)
 {
-    if (first >= g_nevents || second >= g_nevents) return (int)hipErrorInvalidValue;
+    g_timing = 0;
+    if (index >= g_nevents) return (int)hipErrorInvalidValue;
+    if (!g_timed_launches) UQK_TRY(hipEventRecord(g_ev_stop[index], g_stream));
+    return 0;
+}
+
+extern "C" int uqk_op_ns(uint32_t index, uint64_t *ns)
+{
+    if (index >= g_nevents) return (int)hipErrorInvalidValue;
     float ms = 0.f;
-    UQK_TRY(hipEventElapsedTime(&ms, g_events[first], g_events[second]));
+    UQK_TRY(hipEventElapsedTime(&ms, g_ev_start[index], g_ev_stop[index]));
     *ns = (uint64_t)((double)ms * 1e6 + 0.5);
     return 0;
 }

@@ -165,10 +165,14 @@ int uqk_softmax(const void *x, void *y, uint64_t rows, uint32_t width, const voi
 /* Table softmax (code 17) over rows of `width` bytes; table = 256 Q24 values. */
 int uqk_softmax_table(const void *x, void *y, uint64_t rows, uint32_t width, const void *table, int32_t lo, int32_t hi);
 
-/* Timing: a pool of HIP events recorded on the library stream. */
+/* Per-op timing: a start and a stop event for each of `count` ops. Between
+ * time_begin(i) and time_end(i) the launches stamp op i's events with their
+ * own dispatch timestamps (first kernel's start, last kernel's end); op_ns
+ * reads the interval once the stream has passed it. */
 int uqk_events(uint32_t count);
-int uqk_record(uint32_t index);
-int uqk_elapsed_ns(uint32_t first, uint32_t second, uint64_t *ns);
+int uqk_time_begin(uint32_t index);
+int uqk_time_end(uint32_t index);
+int uqk_op_ns(uint32_t index, uint64_t *ns);
 
 #ifdef __cplusplus
 }
