@@ -242,6 +242,23 @@ def conv_add_plan(seed):
     return p.build(z)
 
 
+def pointwise_wide_plan(seed):
+    """A 1x1 conv over 16384-pixel maps (two images give the GPU's widest
+    channel tiles and two row blocks, its register-direct store): channel
+    counts with and without a partly used last tile, post tables, activations
+    and all requantisation ranges."""
+    rng = Rng(seed, 626262)
+    p = Plan(seed)
+    h, w = _pick(rng, [(128, 128), (64, 256), (256, 64)])
+    x = p.input((1, h, w, int(_pick(rng, [16, 32, 64, 96]))), zp=int(rng.integers(1, -128, 127)[0]))
+    lo = int(rng.integers(1, -24, -1)[0])
+    shift = _pick(rng, [(lo, 3), (-12, -4), (-20, -1)])
+    y = p.conv(x, _pick(rng, [64, 80, 96, 112, 128, 192, 256]), k=1, act=_pick(rng, ["none", "relu", "relu6"]),
+               q6=int(rng.integers(1, 1, 200)[0]), lut=_random_lut(p, rng) if _pick(rng, [0, 1]) else None,
+               shift=shift, w_sigma=_pick(rng, [3, 40, 90]), tail_weights=bool(_pick(rng, [0, 1])))
+    return p.build(y)
+
+
 def conv_add_bytes_plan(seed):
     """As conv_add_plan with channel counts that are not multiples of 16 (the
     epilogue's byte path)."""

@@ -11,7 +11,7 @@ import pytest
 import uq_plan as P
 import uq_workloads as W
 from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, dw_mfma_plan, random_plan,
-                       rows_conv_plan, stem_plan)
+                       pointwise_wide_plan, rows_conv_plan, stem_plan)
 from test_oracle_vs_reference import (BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, softmax_table_plan,
                                       transpose_plan)
 from refs import oracle_run
@@ -301,7 +301,7 @@ def test_gather_conv_with_fused_add(lib):
     _assert_same(Graph(plan, lib).run_batch(xin, images), _oracle(plan, xin, images), "gather conv + add")
 
 
-@pytest.mark.parametrize("maker", [dw_mfma_plan, stem_plan, rows_conv_plan])
+@pytest.mark.parametrize("maker", [dw_mfma_plan, stem_plan, rows_conv_plan, pointwise_wide_plan])
 @pytest.mark.parametrize("seed", range(40))
 def test_kernel_shape_fuzz(lib, maker, seed):
     """Matrix-core depthwise (bands, channel groups, small maps), the stem

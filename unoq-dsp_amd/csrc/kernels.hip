@@ -562,6 +562,53 @@ __device__ __forceinline__ void stage_weights(const int8_t *wslice, int kpad, in
     }
 }
 
+// Register-direct store of a k_conv tile computed with the channels as the
+// MFMA rows: a lane holds channels nt*16 + 4*(lane >> 4) + i of pixel
+// rb*16 + (lane & 15). Each (rb, nt) tile is requantised into one packed word
+// per lane, one channel tile's records at a time; then the words of four
+// tiles at a time go through rows_transpose4, after which lane (r, j) holds
+// the 16 channels of pixel r of the group's tile j: one 16-byte store per
+// lane. Needs OC % 16 == 0 and RB * NT a multiple of four.
+template <int RB, int NT, bool HI, bool CORR>
+__device__ __forceinline__ void conv_store_pairs(const ConvArgs &a, const v4i (&acc)[RB][NT], int n0, int lane,
+                                                 long row_base, long row_limit, const int4 *epi_s,
+                                                 const int8_t *lut_s)
+{
+    static_assert((RB * NT) % 4 == 0, "tiles go through the transpose in fours");
+    const int lr = lane & 15, lg = lane >> 4;
+    const int vlo = vgpr(a.lo), vhi = vgpr(a.hi);
+    const bool lut = a.lut != nullptr;
+    int words[RB][NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        Epi e[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) e[i] = load_epi(epi_s, nt * 16 + 4 * lg + i);
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+            int v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[rb][nt][i], e[i], a.yz, vlo, vhi);
+            if (lut) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = lut_s[v[i] + 128];
+            }
+            words[rb][nt] = pack4(v[0], v[1], v[2], v[3]);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < RB * NT / 4; g++) {
+        int r[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) r[q] = words[(g * 4 + q) / NT][(g * 4 + q) % NT];
+        rows_transpose4(r);
+        const int p = g * 4 + lg, rb = p / NT, nt = p - rb * NT;
+        const long row = row_base + rb * 16 + lr;
+        const int cb = n0 + nt * 16;
+        if (row < row_limit && cb < a.oc) *(v4i *)(a.y + row * a.oc + cb) = (v4i){r[0], r[1], r[2], r[3]};
+    }
+}
+
 // Operand ring depth of k_conv: as many K steps in flight as fit about 96
 // registers, a power of two in [2, 8].
 __host__ __device__ constexpr int conv_ring(int rb, int nt)
@@ -590,9 +637,12 @@ __host__ __device__ inline size_t conv_lds(int kpad, int rb, int nt)
     return w > st ? w : st;
 }
 
-template <int RB, int NT, int MODE, int EMODE, bool ADD>
+// DIRECT: channels as the MFMA rows and the register-direct store
+// (conv_store_pairs); instantiated without a fused add.
+template <int RB, int NT, int MODE, int EMODE, bool ADD, bool DIRECT>
 __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
 {
+    static_assert(!(ADD && DIRECT), "the fused add goes through the LDS stage");
     constexpr int R = RB * 16;
     constexpr int STRIDE = NT * 16 + 16;
     constexpr int P = conv_ring(RB, NT);
@@ -665,7 +715,8 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
         for (int nt = 0; nt < NT; nt++)
 #pragma unroll
             for (int rb = 0; rb < RB; rb++)
-                acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0][rb], B[nt], acc[rb][nt], 0, 0, 0);
+                acc[rb][nt] = DIRECT ? __builtin_amdgcn_mfma_i32_16x16x64_i8(B[nt], A[0][rb], acc[rb][nt], 0, 0, 0)
+                                     : __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0][rb], B[nt], acc[rb][nt], 0, 0, 0);
     }
     for (int kc0 = 0; steps > 1 && kc0 < a.kpad; kc0 += kc) {
         const int kn = min(kc, a.kpad - kc0);
@@ -686,7 +737,9 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
                     for (int nt = 0; nt < NT; nt++)
 #pragma unroll
                         for (int rb = 0; rb < RB; rb++)
-                            acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[p][rb], B[nt], acc[rb][nt], 0, 0, 0);
+                            acc[rb][nt] = DIRECT
+                                              ? __builtin_amdgcn_mfma_i32_16x16x64_i8(B[nt], A[p][rb], acc[rb][nt], 0, 0, 0)
+                                              : __builtin_amdgcn_mfma_i32_16x16x64_i8(A[p][rb], B[nt], acc[rb][nt], 0, 0, 0);
                     if (s + P < steps) {
                         const int k1 = (s + P) * 64;
 #pragma unroll
@@ -707,8 +760,12 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a)
         add_s[256 + threadIdx.x] = a.add_tab[256 + threadIdx.x];
     }
     __syncthreads();
-    conv_epilogue_em<RB, NT, EMODE>(a, acc, smem + wave * R * STRIDE, n0, lane, row0, a.M, epi_s, lut_s,
-                                    fused ? add_s : nullptr, rw);
+    if constexpr (DIRECT) {
+        conv_store_pairs<RB, NT, (EMODE & 1) != 0, (EMODE & 2) != 0>(a, acc, n0, lane, row0, a.M, epi_s, lut_s);
+    } else {
+        conv_epilogue_em<RB, NT, EMODE>(a, acc, smem + wave * R * STRIDE, n0, lane, row0, a.M, epi_s, lut_s,
+                                        fused ? add_s : nullptr, rw);
+    }
 }
 
 // Spatial conv with the block's input rows staged in LDS. A block covers up
@@ -1013,22 +1070,29 @@ static void launch_conv_mode(int mode, const ConvArgs &a, dim3 grid, size_t)
     case UQK_PW:
         // The common case: one kernel per requantisation variant and per
         // presence of a fused add.
-#define UQK_PW_EM(ADD)                                                                                          \
-    do {                                                                                                        \
-        switch (a.emode) {                                                                                      \
-        case 0: UQK_LAUNCH((k_conv<RB, NT, UQK_PW, 0, ADD>), grid, dim3(256), lds, g_stream, a); break;  \
-        case 1: UQK_LAUNCH((k_conv<RB, NT, UQK_PW, 1, ADD>), grid, dim3(256), lds, g_stream, a); break;  \
-        case 2: UQK_LAUNCH((k_conv<RB, NT, UQK_PW, 2, ADD>), grid, dim3(256), lds, g_stream, a); break;  \
-        default: UQK_LAUNCH((k_conv<RB, NT, UQK_PW, 3, ADD>), grid, dim3(256), lds, g_stream, a); break; \
-        }                                                                                                       \
+#define UQK_PW_EM(ADD, DIR)                                                                                        \
+    do {                                                                                                           \
+        switch (a.emode) {                                                                                         \
+        case 0: UQK_LAUNCH((k_conv<RB, NT, UQK_PW, 0, ADD, DIR>), grid, dim3(256), lds, g_stream, a); break;  \
+        case 1: UQK_LAUNCH((k_conv<RB, NT, UQK_PW, 1, ADD, DIR>), grid, dim3(256), lds, g_stream, a); break;  \
+        case 2: UQK_LAUNCH((k_conv<RB, NT, UQK_PW, 2, ADD, DIR>), grid, dim3(256), lds, g_stream, a); break;  \
+        default: UQK_LAUNCH((k_conv<RB, NT, UQK_PW, 3, ADD, DIR>), grid, dim3(256), lds, g_stream, a); break; \
+        }                                                                                                          \
     } while (0)
-        if (a.res) UQK_PW_EM(true);
-        else UQK_PW_EM(false);
+        // Register-direct stores when every store is a whole 16 bytes, the
+        // tiles form whole groups of four and no add is fused (a padded
+        // group, or the add applied per transposed word, measured slower
+        // than the LDS stage).
+        if (a.res) UQK_PW_EM(true, false);
+        else if constexpr ((RB * NT) % 4 == 0) {
+            if (a.oc % 16 == 0) UQK_PW_EM(false, true);
+            else UQK_PW_EM(false, false);
+        } else UQK_PW_EM(false, false);
 #undef UQK_PW_EM
         break;
-    case UQK_G16: UQK_LAUNCH((k_conv<RB, NT, UQK_G16, -1, true>), grid, dim3(256), lds, g_stream, a); break;
-    case UQK_G4: UQK_LAUNCH((k_conv<RB, NT, UQK_G4, -1, true>), grid, dim3(256), lds, g_stream, a); break;
-    default: UQK_LAUNCH((k_conv<RB, NT, UQK_G1, -1, true>), grid, dim3(256), lds, g_stream, a); break;
+    case UQK_G16: UQK_LAUNCH((k_conv<RB, NT, UQK_G16, -1, true, false>), grid, dim3(256), lds, g_stream, a); break;
+    case UQK_G4: UQK_LAUNCH((k_conv<RB, NT, UQK_G4, -1, true, false>), grid, dim3(256), lds, g_stream, a); break;
+    default: UQK_LAUNCH((k_conv<RB, NT, UQK_G1, -1, true, false>), grid, dim3(256), lds, g_stream, a); break;
     }
 }
 
