@@ -331,10 +331,10 @@ def stem_plan(seed):
 
 
 def rows_conv_plan(seed):
-    """A spatial conv on 16-channel multiples with OC a multiple of 16 and at
-    most 64 channels per slice: the row-staged kernel at four row blocks with
-    its register-direct epilogue; widths whose rows do and do not fill a
-    block."""
+    """A spatial conv on 16-channel multiples with OC a multiple of 16: the
+    row-staged kernel with its register-direct epilogue, at four row blocks
+    (up to 64 channels per slice) or two (96 and 128: six and eight channel
+    tiles); widths whose rows do and do not fill a block."""
     rng = Rng(seed, 919191)
     p = Plan(seed)
     ic = _pick(rng, [16, 32])
@@ -343,7 +343,7 @@ def rows_conv_plan(seed):
     lo = int(rng.integers(1, -24, -1)[0])
     for shift in ((lo, 3), (-12, -4)):
         try:
-            y = p.conv(x, _pick(rng, [16, 32, 64]), k=_pick(rng, [3, 3, 5]), stride=_pick(rng, [1, 2]),
+            y = p.conv(x, _pick(rng, [16, 32, 64, 96, 128]), k=_pick(rng, [3, 3, 5]), stride=_pick(rng, [1, 2]),
                        act=_pick(rng, ["none", "relu"]), shift=shift, lut=_random_lut(p, rng) if _pick(rng, [0, 1]) else None,
                        w_sigma=_pick(rng, [3, 40, 90]), tail_weights=bool(_pick(rng, [0, 1])))
             return p.build(y)

@@ -928,9 +928,12 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
         }
     }
     const long img0 = n * a.ohw;
-    if constexpr (DIRECT) {
+    if constexpr (DIRECT && RB % 4 == 0) {
         conv_store_direct<RB, NT, (EMODE & 1) != 0, (EMODE & 2) != 0>(a, acc, n0, lane, img0 + p0 + wave * R,
                                                                        img0 + pend, epi_s, lut_s);
+    } else if constexpr (DIRECT) {
+        conv_store_pairs<RB, NT, (EMODE & 1) != 0, (EMODE & 2) != 0>(a, acc, n0, lane, img0 + p0 + wave * R,
+                                                                      img0 + pend, epi_s, lut_s);
     } else {
         const int rw[RB][NT] = {};
         conv_epilogue_em<RB, NT, EMODE>(a, acc, stage, n0, lane, img0 + p0 + wave * R, img0 + pend, epi_s, lut_s,
@@ -1107,13 +1110,21 @@ static void launch_conv_nt(int nt, int mode, const ConvArgs &a, dim3 grid, size_
     }
 }
 
+// Whether k_conv_rows stores from registers (no LDS output stage): whole
+// 16-byte stores, and row blocks (conv_store_direct) or channel tiles
+// (conv_store_pairs) that go through the transpose in fours.
+static bool rows_direct(int rb, int nt, int oc)
+{
+    return oc % 16 == 0 && (rb % 4 == 0 || (rb * nt) % 4 == 0);
+}
+
 template <int RB>
 static void launch_rows_nt(int nt, int mode, const ConvArgs &a, dim3 grid, size_t lds)
 {
-    // Register-direct epilogue (no LDS output stage) with four row blocks;
-    // uqk_conv picks rb = 4 only when OC % 16 == 0 (whole 16-byte stores).
-    constexpr bool DIR = RB % 4 == 0;
-#define UQK_ROWS_EM(NT, W)                                                                                      \
+    // Register-direct epilogue (no LDS output stage) as rows_direct decides;
+    // uqk_conv picks rb = 4 only when OC % 16 == 0, and every even NT makes
+    // two row blocks whole groups of four tiles.
+#define UQK_ROWS_EM(NT, W, DIR)                                                                                 \
     do {                                                                                                        \
         switch (a.emode) {                                                                                      \
         case 0: UQK_LAUNCH((k_conv_rows<RB, NT, W, 0, DIR>), grid, dim3(256), lds, g_stream, a); break; \
@@ -1122,10 +1133,16 @@ static void launch_rows_nt(int nt, int mode, const ConvArgs &a, dim3 grid, size_
         default: UQK_LAUNCH((k_conv_rows<RB, NT, W, 3, DIR>), grid, dim3(256), lds, g_stream, a); break; \
         }                                                                                                       \
     } while (0)
+#define UQK_ROWS_DIR(NT, W)                                                                                     \
+    do {                                                                                                        \
+        if constexpr (RB % 4 == 0) UQK_ROWS_EM(NT, W, true);                                                    \
+        else if (rows_direct(RB, NT, a.oc)) UQK_ROWS_EM(NT, W, true);                                           \
+        else UQK_ROWS_EM(NT, W, false);                                                                         \
+    } while (0)
 #define UQK_ROWS_LAUNCH(NT)                                                                                     \
     do {                                                                                                        \
-        if (mode == UQK_ROWS16) UQK_ROWS_EM(NT, false);                                                         \
-        else UQK_ROWS_EM(NT, true);                                                                             \
+        if (mode == UQK_ROWS16) UQK_ROWS_DIR(NT, false);                                                        \
+        else UQK_ROWS_DIR(NT, true);                                                                            \
     } while (0)
     switch (nt) {
     case 2: UQK_ROWS_LAUNCH(2); break;
@@ -1134,6 +1151,7 @@ static void launch_rows_nt(int nt, int mode, const ConvArgs &a, dim3 grid, size_
     default: UQK_ROWS_LAUNCH(8); break;
     }
 #undef UQK_ROWS_LAUNCH
+#undef UQK_ROWS_DIR
 #undef UQK_ROWS_EM
 }
 
@@ -1160,7 +1178,7 @@ static size_t rows_lds(const UQKSpatial *d, int rb)
 {
     int span;
     rows_tile(d, rb, &span);
-    const bool direct = rb % 4 == 0 && d->oc % 16 == 0;
+    const bool direct = rows_direct(rb, d->nt, d->oc);
     const int rows_max = (span - 1) * d->sh + (d->kh - 1) * d->dh + 1;
     const int cols = (d->ow - 1) * d->sw + (d->kw - 1) * d->dw + 1;
     const int ndelta = d->mode == UQK_ROWS16 ? d->K / 16 : d->K / 4;
