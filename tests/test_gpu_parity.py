@@ -287,6 +287,42 @@ def test_split_batch_matches_single_stream(lib, monkeypatch, name, images):
         _assert_same(outs["2"][i * ob:(i + 1) * ob], _oracle(plan, x[i * ib:(i + 1) * ib], 1), f"{name} image {i}")
 
 
+def test_split_batches_continue_across_calls(lib, monkeypatch):
+    """Consecutive identical device batches keep their two slices on their
+    own streams without joining; a batch on other buffers, a snapshot taken
+    straight after an enqueue, and a host-buffer run in between all see
+    finished results, equal to one stream's."""
+    plan, _ = W.mnv4()
+    images = 130
+    x1, x2 = P.random_input(plan, images, 51), P.random_input(plan, images, 52)
+    recs = P.tensor_records(plan)
+    t = _fused_conv_outputs(plan)[0]
+    monkeypatch.setenv("UQ_STREAMS", "1")
+    g1 = Graph(plan, lib)
+    y1, y2 = g1.run_batch(x1, images), g1.run_batch(x2, images)
+    snap2 = g1.snapshot_images(t, images * recs[t][1])
+    monkeypatch.setenv("UQ_STREAMS", "2")
+    g = Graph(plan, lib)
+    bufs = [(DeviceBuffer(lib, x1.nbytes), DeviceBuffer(lib, images * g.output_bytes)) for _ in range(2)]
+    for (din, _), x in zip(bufs, (x1, x2)):
+        din.upload(x)
+    order = [0, 0, 0, 1, 0, 1, 1]
+    for k in order:
+        assert lib.ug_enqueue_device(bufs[k][0].ptr, bufs[k][1].ptr, images) == 0
+    assert lib.ug_synchronize() == 0
+    _assert_same(bufs[0][1].download(), y1, "batch 1 after interleaved enqueues")
+    _assert_same(bufs[1][1].download(), y2, "batch 2 after interleaved enqueues")
+    assert lib.ug_enqueue_device(bufs[1][0].ptr, bufs[1][1].ptr, images) == 0
+    _assert_same(g.snapshot_images(t, images * recs[t][1]), snap2, f"snapshot of tensor {t} right after an enqueue")
+    assert lib.ug_enqueue_device(bufs[0][0].ptr, bufs[0][1].ptr, images) == 0
+    _assert_same(g.run_batch(x2, images), y2, "host-buffer run after an enqueue")
+    assert lib.ug_synchronize() == 0
+    _assert_same(bufs[0][1].download(), y1, "batch 1 after the host-buffer run")
+    for din, dout in bufs:
+        din.free()
+        dout.free()
+
+
 def test_gather_conv_with_fused_add(lib):
     """A 3x3 conv too wide for row staging (80x80x128, K = 1152: the gather
     kernel) followed by a residual add of its input: the add runs in the

@@ -65,6 +65,9 @@ static struct {
     uint16_t fuse_of_tensor[UG_MAX_T];   /* group index + 1 of an inner tensor */
     uint8_t ext[UG_MAX_T];               /* G.ptr[t] is a caller buffer this run */
     int slices;                          /* UQ_STREAMS at load: image slices of a batch, 0 = default */
+    int split_open, split_n;             /* the last split batch's side stream is not joined yet */
+    uint32_t split_images;               /* ... its image count, input and output addresses */
+    const void *split_in, *split_out;
     uint32_t ngroups;
     Group groups[UG_MAX_OP / 2 + 1];
     uint8_t *pipe_in[2], *pipe_out[2]; /* device chunk buffers of the pipelined batch */
@@ -747,6 +750,7 @@ static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
 }
 
 static int enqueue_op(uint32_t i, uint32_t images);
+static int settle(void);
 
 /* Consumers of each activation tensor (operands a/b of every op, pack lists). */
 static void count_users(uint16_t *users)
@@ -935,6 +939,10 @@ static int prepare_device(void)
 
 int ug_load(const void *blob, uint32_t len)
 {
+    if (G.split_open) {
+        (void)settle();
+        (void)uqk_sync();
+    }
     G.ready = 0;
     G.profile_enabled = 0;
     G.stream_active = 0;
@@ -975,7 +983,7 @@ uint32_t ug_op_count(void) { return G.ready ? G.h.no : 0; }
 static int ensure_capacity(uint32_t images)
 {
     if (images <= G.capacity) return 0;
-    if (uqk_sync()) return 24;
+    if (settle() || uqk_sync()) return 24;
     for (uint32_t t = 0; t < G.h.nt; t++) {
         uqk_free(G.act[t]);
         G.act[t] = NULL;
@@ -1049,21 +1057,48 @@ static int slice_count(uint32_t images)
     return n;
 }
 
+/* Join the side stream of the last split batch into the library stream, if
+ * it may still hold work of that batch (see enqueue_ops). Every entry point
+ * that puts other work on the library stream, reads results or changes
+ * buffers calls this first. */
+static int settle(void)
+{
+    if (!G.split_open) return 0;
+    G.split_open = 0;
+    return uqk_split_join(G.split_n) ? 24 : 0;
+}
+
 /* Enqueue the whole plan. A large batch runs as image slices on separate
  * compute streams, op by op in turn, so that the launches of one slice
  * overlap the latency and tail of the other's: every op works image by
  * image, and each slice sees the batch's buffers offset by its first image
  * (shared constants are not offset). Each slice keeps its own address table
  * across ops, since internal copies alias their source (enqueue_op, code 5).
- * Afterwards G.ptr is slice 0's table, the addresses of the whole batch. */
+ * Afterwards G.ptr is slice 0's table, the addresses of the whole batch.
+ *
+ * The side stream is not joined back at the end: the next identical batch
+ * (same slices, image count, input and output buffers) continues on each
+ * stream, where each slice reads and writes the same images as before, so
+ * the two streams drift apart and one slice's bandwidth-bound layers overlap
+ * the other's latency-bound ones. Anything else settles first (the side
+ * stream joins the library stream; uqk_sync waits for both). */
 static int enqueue_ops(uint32_t images)
 {
     const int n = slice_count(images);
     int rc = 0;
     uint32_t next = 0;
     if (n == 1) {
+        if (settle()) return 24;
         return enqueue_range(0, G.h.no, images, &next);
     }
+    const int cont = G.split_open && G.split_n == n && G.split_images == images &&
+                     G.split_in == G.ptr[G.h.input] && G.split_out == G.ptr[G.h.output];
+    if (!cont && (settle() || uqk_split_fork(n))) return 24;
+    G.split_open = 1;
+    G.split_n = n;
+    G.split_images = images;
+    G.split_in = G.ptr[G.h.input];
+    G.split_out = G.ptr[G.h.output];
     static uint8_t *tab[UQK_MAX_SLICES][UG_MAX_T];
     uint32_t first[UQK_MAX_SLICES + 1];
     for (int k = 0; k <= n; k++) first[k] = (uint32_t)((uint64_t)images * (uint32_t)k / (uint32_t)n);
@@ -1071,16 +1106,15 @@ static int enqueue_ops(uint32_t images)
         for (uint32_t t = 0; t < G.h.nt; t++)
             tab[k][t] = G.ts[t].flags && !G.bcast[t] ? G.ptr[t] : G.ptr[t] + (size_t)first[k] * G.ts[t].bytes;
     const size_t tb = sizeof(uint8_t *) * G.h.nt;
-    if (uqk_split_begin(n)) return 24;
     for (uint32_t i = 0; i < G.h.no && !rc; i = next) {
         for (int k = n - 1; k >= 0 && !rc; k--) {
             memcpy(G.ptr, tab[k], tb);
-            uqk_split_use(k);
+            uqk_split_use(k, n);
             rc = enqueue_range(i, i + 1, first[k + 1] - first[k], &next);
             memcpy(tab[k], G.ptr, tb);
         }
     }
-    if (uqk_split_end(n) && !rc) rc = 24;
+    uqk_split_use(0, 1);
     memcpy(G.ptr, tab[0], tb);
     /* Fused groups record the input and image count of the whole batch. */
     for (uint32_t g = 0; g < G.ngroups; g++)
@@ -1270,7 +1304,7 @@ int ug_run_batch(const void *input, uint64_t ni, void *output, uint64_t no, uint
     if (!G.ready || !input || !output || !images || ni != (uint64_t)images * ug_input_bytes() ||
         no != (uint64_t)images * ug_output_bytes())
         return 22;
-    if (ensure_capacity(images)) return fail(24);
+    if (settle() || ensure_capacity(images)) return fail(24);
     bind_pointers(NULL, NULL);
     if (uqk_h2d(G.ptr[G.h.input], input, ni)) return fail(24);
     if (enqueue_ops(images)) return fail(24);
@@ -1298,6 +1332,8 @@ int ug_enqueue_device(const void *d_input, void *d_output, uint32_t images)
     if (ensure_capacity(images)) return fail(24);
     bind_pointers(d_input, d_output);
     if (enqueue_ops(images)) return fail(24);
+    /* A copy of the output on the library stream needs the whole batch. */
+    if (G.ptr[G.h.output] != (uint8_t *)d_output && settle()) return fail(24);
     if (deliver_output_device(d_output, images)) return fail(24);
     G.last_images = images;
     return 0;
@@ -1306,6 +1342,7 @@ int ug_enqueue_device(const void *d_input, void *d_output, uint32_t images)
 int ug_synchronize(void)
 {
     if (uqk_sync()) return fail(24);
+    G.split_open = 0;                    /* both streams are idle */
     return finish_profile() ? fail(24) : 0;
 }
 
@@ -1326,6 +1363,7 @@ int ug_run_batch_pipelined(const void *input, uint64_t ni, void *output, uint64_
     if (!G.ready || !input || !output || !images || ni != (uint64_t)images * ug_input_bytes() ||
         no != (uint64_t)images * ug_output_bytes())
         return 22;
+    if (settle()) return fail(24);
     const Tensor *t = G.ts + G.h.output;
     /* Auto: chunks of at least 256 images (smaller launches underfill the
      * chip, which costs more than the overlap gains), pipelined from 512. */
@@ -1417,6 +1455,7 @@ void ug_close(void *ptr)
 {
     Session *s = ptr;
     if (!s || s != g_session) return;
+    (void)settle();
     (void)uqk_sync();
     session_release(s);
     g_session = NULL;
@@ -1495,6 +1534,7 @@ int ug_infer(void *ptr, const void *in, uint32_t ni, void *out, uint32_t no)
     if (!s || s != g_session || !in || !out || ni != s->ni || no != s->no) return 1003;
     if (!s->pipeline || G.profile_enabled || G.ts[G.h.output].flags) return ug_run(in, ni, out, no);
     if (!G.ready || ug_input_bytes() != ni || ug_output_bytes() != no) return 22;
+    if (settle()) return fail(24);
     if ((!s->graph || s->generation != G.generation) && session_capture(s)) return fail(24);
     memcpy(s->h_in, in, ni);
     if (uqk_h2d(s->d_in, s->h_in, ni) || uqk_graph_launch(s->graph) || uqk_d2h(s->h_out, s->d_out, no) || uqk_sync())
@@ -1530,7 +1570,7 @@ int ug_snapshot_images(uint32_t index, void *out, uint64_t bytes)
         return 0;
     }
     if (!G.last_images || bytes != (uint64_t)G.last_images * t->bytes) return 22;
-    if (materialize_group(index)) return fail(24);
+    if (settle() || materialize_group(index)) return fail(24);
     if (uqk_d2h(out, G.ptr[index], bytes) || uqk_sync()) return fail(24);
     return 0;
 }
@@ -1547,7 +1587,7 @@ int ug_snapshot(uint32_t index, void *out, uint32_t bytes)
         memcpy(out, G.arena + t->offset, bytes); /* arena contents before any run */
         return 0;
     }
-    if (materialize_group(index)) return fail(24);
+    if (settle() || materialize_group(index)) return fail(24);
     if (uqk_d2h(out, G.ptr[index], bytes) || uqk_sync()) return fail(24);
     return 0;
 }
@@ -1584,18 +1624,19 @@ void *ug_device_alloc(uint64_t bytes)
 
 int ug_device_free(void *d)
 {
+    (void)settle();
     uqk_free(d);
     return 0;
 }
 
 int ug_device_upload(void *d_dst, const void *src, uint64_t bytes)
 {
-    if (uqk_init() || uqk_h2d(d_dst, src, (size_t)bytes) || uqk_sync()) return 24;
+    if (uqk_init() || settle() || uqk_h2d(d_dst, src, (size_t)bytes) || uqk_sync()) return 24;
     return 0;
 }
 
 int ug_device_download(void *dst, const void *d_src, uint64_t bytes)
 {
-    if (uqk_init() || uqk_d2h(dst, d_src, (size_t)bytes) || uqk_sync()) return 24;
+    if (uqk_init() || settle() || uqk_d2h(dst, d_src, (size_t)bytes) || uqk_sync()) return 24;
     return 0;
 }

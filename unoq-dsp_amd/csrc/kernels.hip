@@ -2918,22 +2918,27 @@ extern "C" int uqk_init(void)
 }
 
 // A batch split into image slices, one compute stream each: slice 0 on the
-// main stream, slice k on side stream k - 1. The side streams start after
-// everything already queued on the main stream; split_end makes the main
-// stream wait for all of them, so later work (and uqk_sync) sees the whole
+// main stream, slice k on side stream k - 1. split_fork orders the side
+// streams after everything already queued on the main stream; split_use
+// sends the following launches to one slice's stream (and tells the launch
+// heuristics how many slices run side by side); split_join makes the main
+// stream wait for the side streams, so that later work on it sees the whole
 // batch.
-extern "C" int uqk_split_begin(int slices)
+extern "C" int uqk_split_fork(int slices)
 {
     if (slices < 1 || slices > UQK_MAX_SLICES) return (int)hipErrorInvalidValue;
-    g_live_slices = slices;
     UQK_TRY(hipEventRecord(g_fork, g_main));
     for (int k = 0; k < slices - 1; k++) UQK_TRY(hipStreamWaitEvent(g_side[k], g_fork, 0));
     return 0;
 }
 
-extern "C" void uqk_split_use(int slice) { g_stream = slice > 0 ? g_side[slice - 1] : g_main; }
+extern "C" void uqk_split_use(int slice, int slices)
+{
+    g_stream = slice > 0 ? g_side[slice - 1] : g_main;
+    g_live_slices = slices;
+}
 
-extern "C" int uqk_split_end(int slices)
+extern "C" int uqk_split_join(int slices)
 {
     g_stream = g_main;
     g_live_slices = 1;
@@ -2976,6 +2981,7 @@ extern "C" int uqk_sync_all(void)
     UQK_TRY(hipStreamSynchronize(g_copy[0]));
     UQK_TRY(hipStreamSynchronize(g_main));
     UQK_TRY(hipStreamSynchronize(g_copy[1]));
+    for (int k = 0; k < UQK_MAX_SLICES - 1; k++) UQK_TRY(hipStreamSynchronize(g_side[k]));
     return 0;
 }
 
@@ -3064,7 +3070,8 @@ extern "C" int uqk_d2d_2d(void *dst, size_t dpitch, const void *src, size_t spit
 
 extern "C" int uqk_sync(void)
 {
-    UQK_TRY(hipStreamSynchronize(g_stream));
+    UQK_TRY(hipStreamSynchronize(g_main));
+    for (int k = 0; k < UQK_MAX_SLICES - 1; k++) UQK_TRY(hipStreamSynchronize(g_side[k]));
     return 0;
 }
 

@@ -102,16 +102,17 @@ int uqk_pipe_wait(int stream, int event);
 int uqk_sync_all(void);
 
 /* Image slices of one batch on separate compute streams (at most
- * UQK_MAX_SLICES): split_begin orders the side streams after the main
- * stream's queued work, split_use(k) sends the following launches to slice
- * k's stream, split_end joins the side streams into the main stream and
- * makes it current again. Two: the main stream, the two transfer streams
- * and one side stream are HIP's default four hardware queues (more streams
- * would share a queue, and more queues measured far slower). */
+ * UQK_MAX_SLICES): split_fork orders the side streams after the main
+ * stream's queued work, split_use(k, n) sends the following launches to
+ * slice k's stream (n slices running side by side), split_join makes the
+ * main stream wait for the side streams and current again. Two: the main
+ * stream, the two transfer streams and one side stream are HIP's default
+ * four hardware queues (more streams would share a queue, and more queues
+ * measured far slower). uqk_sync waits for the main and side streams. */
 #define UQK_MAX_SLICES 2
-int uqk_split_begin(int slices);
-void uqk_split_use(int slice);
-int uqk_split_end(int slices);
+int uqk_split_fork(int slices);
+void uqk_split_use(int slice, int slices);
+int uqk_split_join(int slices);
 void *uqk_host_alloc(size_t bytes);                   /* pinned (hipHostMalloc) */
 void uqk_host_free(void *p);
 
