@@ -563,7 +563,7 @@ static ConvPlan conv_plan(const Op *o)
         memset(&t, 0, sizeof t);
         t.ow = q[11]; t.sw = q[3]; t.kh = q[0]; t.kw = q[1]; t.sh = q[2]; t.dh = q[4]; t.dw = q[5];
         t.ic = ic; t.K = kw4; t.nt = c.nt; t.mode = rows_mode;
-        if (uqk_conv_rows_lds(&t, 2) <= 65536) {
+        if (uqk_conv_rows_ok(&t)) {
             c.mode = rows_mode;
             c.icp = icp;
             c.K = kw4;

@@ -1174,11 +1174,11 @@ static int rows_tile(const UQKSpatial *d, int rb, int *span)
 // Dynamic LDS of k_conv_rows at rb row blocks per wave: the staged tile, the
 // offset table and, unless the epilogue stores straight from registers
 // (rb = 4, OC % 16 == 0), the output stage.
-static size_t rows_lds(const UQKSpatial *d, int rb)
+static size_t rows_lds(const UQKSpatial *d, int rb, bool with_stage = false)
 {
     int span;
     rows_tile(d, rb, &span);
-    const bool direct = rows_direct(rb, d->nt, d->oc);
+    const bool direct = !with_stage && rows_direct(rb, d->nt, d->oc);
     const int rows_max = (span - 1) * d->sh + (d->kh - 1) * d->dh + 1;
     const int cols = (d->ow - 1) * d->sw + (d->kw - 1) * d->dw + 1;
     const int ndelta = d->mode == UQK_ROWS16 ? d->K / 16 : d->K / 4;
@@ -1188,6 +1188,13 @@ static size_t rows_lds(const UQKSpatial *d, int rb)
 }
 
 extern "C" size_t uqk_conv_rows_lds(const UQKSpatial *d, int rb) { return rows_lds(d, rb); }
+
+// Plan-time choice of the row-staged kernel: its two-row-block tile, counted
+// with an output stage, within 64 KiB. Layers past that (wide K, such as a
+// 3x3 over 128 channels at 80x80) measured faster as gathers (k_conv G16:
+// 857 against 584 TOPS), so the register-direct epilogue's smaller footprint
+// does not move them.
+extern "C" int uqk_conv_rows_ok(const UQKSpatial *d) { return rows_lds(d, 2, true) <= 65536; }
 
 static int conv_launch(const UQKSpatial *d, const void *x, void *y, uint32_t batches, const UQKAdd *add);
 

@@ -77,6 +77,9 @@ int uqk_conv_stem_ok(const UQKSpatial *d);
 
 /* Dynamic LDS bytes k_conv_rows needs for a layer at rb row blocks per wave. */
 size_t uqk_conv_rows_lds(const UQKSpatial *d, int rb);
+/* Whether a conv layer runs on k_conv_rows (chosen when the plan is loaded;
+ * reads the fields uqk_conv_rows_lds reads). */
+int uqk_conv_rows_ok(const UQKSpatial *d);
 
 int uqk_init(void);
 int uqk_device_count(void);
