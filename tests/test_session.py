@@ -128,7 +128,8 @@ def test_mailbox_graph_follows_reload(lib):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,images,chunk", [("pointwise", 7, 3), ("pointwise", 8, 2), ("mnv4", 256, 64),
-                                               ("mnv4", 100, 0), ("yolo", 64, 16), ("dw3s2", 64, 24)])
+                                               ("mnv4", 100, 0), ("yolo", 64, 16), ("dw3s2", 64, 24),
+                                               ("mnv4", 512, 256)])
 @pytest.mark.parametrize("pinned", [False, True])
 def test_pipelined_batch(lib, name, images, chunk, pinned):
     plan, _ = W.WORKLOADS[name]()
@@ -149,6 +150,10 @@ def test_pipelined_batch(lib, name, images, chunk, pinned):
         rc = lib.ug_run_batch_pipelined(x.ctypes.data, x.nbytes, y.ctypes.data, y.nbytes, images, chunk)
     assert rc == 0
     samples = range(images) if images <= 8 else (0, chunk - 1 if chunk else 1, images // 2, images - 1)
+    if chunk >= 128:
+        # Chunks this large run as two image slices on two streams: images
+        # of the second slice of each chunk too.
+        samples = sorted(set(samples) | {chunk // 2 + 1, chunk + chunk // 2 + 3})
     for j in samples:
         np.testing.assert_array_equal(y[j * ob:(j + 1) * ob], oracle_run(plan, x[j * ib:(j + 1) * ib], 1, ob),
                                       err_msg=f"{name} image {j}")

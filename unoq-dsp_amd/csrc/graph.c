@@ -1307,7 +1307,8 @@ int ug_run_batch(const void *input, uint64_t ni, void *output, uint64_t no, uint
     if (settle() || ensure_capacity(images)) return fail(24);
     bind_pointers(NULL, NULL);
     if (uqk_h2d(G.ptr[G.h.input], input, ni)) return fail(24);
-    if (enqueue_ops(images)) return fail(24);
+    /* The copy back runs on the library stream: it needs both slices. */
+    if (enqueue_ops(images) || settle()) return fail(24);
     const Tensor *t = G.ts + G.h.output;
     if (t->flags) {
         if (uqk_sync()) return fail(24);
@@ -1400,7 +1401,9 @@ int ug_run_batch_pipelined(const void *input, uint64_t ni, void *output, uint64_
         if (uqk_pipe_wait(0, slot)) return fail(24);
         if (k >= 2 && uqk_pipe_wait(0, 4 + slot)) return fail(24);
         bind_pointers(G.pipe_in[slot], G.pipe_out[slot]);
-        if (enqueue_ops(nk) || deliver_output_device(G.pipe_out[slot], nk)) return fail(24);
+        /* The chunk's completion event is recorded on the library stream:
+         * join the side stream first. */
+        if (enqueue_ops(nk) || settle() || deliver_output_device(G.pipe_out[slot], nk)) return fail(24);
         if (uqk_pipe_record(2 + slot, 0)) return fail(24);
         if (uqk_pipe_wait(2, 2 + slot)) return fail(24);
         if (uqk_copy_on(2, dst, G.pipe_out[slot], (size_t)nk * ob, 0) || uqk_pipe_record(4 + slot, 2)) return fail(24);
