@@ -1,8 +1,8 @@
 /* CPU restatement of the reference's INT8 NHWC vision path.
  *
  * TEST INFRASTRUCTURE ONLY. Tests, the smoke check and the benchmark's CPU
- * baseline leg load this file's library as the checker; the GPU library never
- * links or calls it.
+ * baseline leg load this file's library to check results against; the GPU
+ * library never links or calls it.
  *
  * Every function follows the *generic* (macro-free) semantics of the
  * reference runtime; each cites the file:line it restates. Scalar loops on

@@ -1,5 +1,5 @@
-"""Test-side bindings of the checkers: our CPU oracle (oracle/liboracle.so) and
-the reference's own portable C runtime built from its sources (oracle/_ref).
+"""Test-side bindings of the CPU oracle (oracle/liboracle.so) and of the
+reference's own portable C runtime built from its sources (oracle/_ref).
 
 Only tests, the smoke check and the benchmark's CPU baseline import this."""
 import ctypes as C
