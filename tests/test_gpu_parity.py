@@ -5,6 +5,8 @@ Small image counts are compared in full; full-batch runs (256 / 512 images)
 are checked through size-independent properties: every sampled image of the
 batch equals that image run alone through the oracle, and a batch result is
 identical between the host and the device entry points."""
+import struct
+
 import numpy as np
 import pytest
 
@@ -321,6 +323,34 @@ def test_split_batches_continue_across_calls(lib, monkeypatch):
     for din, dout in bufs:
         din.free()
         dout.free()
+
+
+@pytest.mark.parametrize("images", [3, 130])
+def test_device_path_output_reshape(lib, images):
+    """MobileNetV4 ends in a reshape (op 5) of the classifier's output, which
+    on the device path lands in the caller's buffer: the output and a
+    snapshot of the reshaped tensor match the oracle, on one stream and on
+    two slices."""
+    plan, _ = W.mnv4()
+    ops, recs = P.op_records(plan), P.tensor_records(plan)
+    out = struct.unpack_from("<I", plan, 24)[0]          # header: output tensor index
+    last = [o for o in ops if o[0] == 5 and o[3] == out]
+    assert last, "the plan's output is a reshape"
+    src = last[0][1]
+    x = P.random_input(plan, images, 23)
+    g = Graph(plan, lib)
+    din, dout = DeviceBuffer(lib, x.nbytes), DeviceBuffer(lib, images * g.output_bytes)
+    din.upload(x)
+    assert lib.ug_run_device(din.ptr, dout.ptr, images) == 0
+    ib, ob = g.input_bytes, g.output_bytes
+    y = dout.download()
+    for j in (0, images // 2, images - 1):
+        _assert_same(y[j * ob:(j + 1) * ob], _oracle(plan, x[j * ib:(j + 1) * ib], 1), f"image {j}")
+    if images <= 3:
+        _, want = oracle_run(plan, x, images, P.output_bytes(plan), snap=src, snap_bytes=images * recs[src][1])
+        _assert_same(g.snapshot_images(src, images * recs[src][1]), want, f"snapshot of tensor {src}")
+    din.free()
+    dout.free()
 
 
 def test_gather_conv_with_fused_add(lib):
