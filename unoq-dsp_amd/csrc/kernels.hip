@@ -941,6 +941,38 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
     }
 }
 
+// Row blocks G0 .. min(G0 + 4, NRB) - 1 of a stem wave: each lane's window
+// (five aligned LDS words byte-aligned into its 16-byte K slice), one MFMA
+// per channel tile, then the group's requantised store. The kernel runs its
+// row blocks in these groups of four (the transpose's group), so only 16 NT
+// accumulator registers are live (70 instead of 82 VGPRs at NT = 2).
+template <int NT, int NRB, bool HI, bool CORR, int G0>
+__device__ __forceinline__ void stem_group(const ConvArgs &a, const v4i (&B)[NT], const int8_t *smem, int wbase,
+                                           int step, int ox0, int lane, int n0, long rbase, long rlimit,
+                                           const int4 *epi_s, const int8_t *lut_s)
+{
+    constexpr int NG = NRB - G0 < 4 ? NRB - G0 : 4;
+    const int lr = lane & 15;
+    v4i acc[4][NT];
+#pragma unroll
+    for (int q = 0; q < NG; q++) {
+        const int ox = min(ox0 + (G0 + q) * 16 + lr, a.ow - 1);
+        const int off = wbase + __mul24(ox, step);
+        const int *p = (const int *)(smem + (off & ~3));
+        const int w0 = p[0], w1 = p[1], w2 = p[2], w3 = p[3], w4 = p[4];
+        const unsigned sh = (unsigned)off;             // byte-align uses the low two bits
+        const v4i A = {(int)__builtin_amdgcn_alignbyte((unsigned)w1, (unsigned)w0, sh),
+                       (int)__builtin_amdgcn_alignbyte((unsigned)w2, (unsigned)w1, sh),
+                       (int)__builtin_amdgcn_alignbyte((unsigned)w3, (unsigned)w2, sh),
+                       (int)__builtin_amdgcn_alignbyte((unsigned)w4, (unsigned)w3, sh)};
+        // Channels as the MFMA rows (weights in A), pixels as its columns.
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+            acc[q][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(B[nt], A, (v4i){0, 0, 0, 0}, 0, 0, 0);
+    }
+    conv_store_direct<4, NT, HI, CORR, NG>(a, acc, n0, lane, rbase + G0 * 16, rlimit, epi_s, lut_s);
+}
+
 // Stem convolution (few input channels, kh <= 4, kw * IC <= 16, no column
 // dilation). The K step is one kernel row per 16-lane group: lane group lg
 // holds kernel row ky = lg, and its 16-byte K slice is the kw * IC
@@ -958,7 +990,6 @@ __global__ __launch_bounds__(256) void k_conv_rows(ConvArgs a)
 template <int NT, int NRB, int EMODE>
 __global__ __launch_bounds__(256) void k_conv_stem(ConvArgs a)
 {
-    constexpr int RB = (NRB + 3) & ~3;
     constexpr bool HI = EMODE & 1, CORR = EMODE & 2;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     __shared__ __attribute__((aligned(4))) int8_t lut_s[256];
@@ -1018,31 +1049,13 @@ __global__ __launch_bounds__(256) void k_conv_stem(ConvArgs a)
     const int wbase = 16 + (wave * a.sh + ky * a.dh) * rs - a.pl * a.ic;
     const int step = a.sw * a.ic;                      // window bytes between neighbouring pixels
     __syncthreads();
-    v4i A[NRB];
-#pragma unroll
-    for (int rb = 0; rb < NRB; rb++) {
-        const int ox = min(ox0 + rb * 16 + lr, a.ow - 1);
-        const int off = wbase + __mul24(ox, step);
-        const int *p = (const int *)(smem + (off & ~3));
-        const int w0 = p[0], w1 = p[1], w2 = p[2], w3 = p[3], w4 = p[4];
-        const unsigned sh = (unsigned)off;             // byte-align uses the low two bits
-        A[rb] = (v4i){(int)__builtin_amdgcn_alignbyte((unsigned)w1, (unsigned)w0, sh),
-                      (int)__builtin_amdgcn_alignbyte((unsigned)w2, (unsigned)w1, sh),
-                      (int)__builtin_amdgcn_alignbyte((unsigned)w3, (unsigned)w2, sh),
-                      (int)__builtin_amdgcn_alignbyte((unsigned)w4, (unsigned)w3, sh)};
-    }
-    // Channels as the MFMA rows (weights in A), pixels as its columns.
-    v4i acc[RB][NT];
-#pragma unroll
-    for (int rb = 0; rb < NRB; rb++)
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++)
-            acc[rb][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(B[nt], A[rb], (v4i){0, 0, 0, 0}, 0, 0, 0);
     // Output pixels of this wave: its output row, ox0 .. min(ox0 + seg_rb * 16, ow).
     const long rbase = ((long)n * a.oh + oy) * a.ow + ox0;
     const int send = min(ox0 + a.seg_rb * 16, a.ow);
     const long rlimit = row_ok ? ((long)n * a.oh + oy) * a.ow + send : rbase;
-    conv_store_direct<RB, NT, HI, CORR, NRB>(a, acc, n0, lane, rbase, rlimit, epi_s, lut_s);
+    stem_group<NT, NRB, HI, CORR, 0>(a, B, smem, wbase, step, ox0, lane, n0, rbase, rlimit, epi_s, lut_s);
+    if constexpr (NRB > 4)
+        stem_group<NT, NRB, HI, CORR, 4>(a, B, smem, wbase, step, ox0, lane, n0, rbase, rlimit, epi_s, lut_s);
 }
 
 // Dynamic LDS of k_conv_stem (a 16-byte lead, the staged rows each followed
