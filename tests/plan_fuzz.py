@@ -350,3 +350,41 @@ def rows_conv_plan(seed):
         except ValueError:
             continue
     raise AssertionError("unreachable")
+
+
+def gemm_plan(seed):
+    """A conv the large-tile GEMM takes: pointwise over 256-960 channels (K
+    not always a multiple of 64) or 3x3/5x5 over 64/128 channels (implicit
+    im2col; strides, dilation, SAME and explicit padding), OC from 16 to 400
+    in steps of 16 (tails against 128- and 256-channel tiles), pixel counts
+    that are not multiples of the 256-pixel tile, post tables, activations
+    and all requantisation ranges."""
+    rng = Rng(seed, 565656)
+    p = Plan(seed)
+    pointwise = bool(_pick(rng, [0, 1]))
+    if pointwise:
+        ic = _pick(rng, [256, 272, 528, 960])
+        h, w = _pick(rng, [(7, 7), (9, 13), (16, 16), (5, 37)])
+        k, stride, dilation = 1, 1, 1
+    else:
+        ic = _pick(rng, [64, 128])
+        h, w = _pick(rng, [(7, 7), (9, 13), (16, 16), (20, 11)])
+        k, stride, dilation = _pick(rng, [3, 3, 5]), _pick(rng, [1, 2]), _pick(rng, [1, 1, 2])
+    x = p.input((1, h, w, ic), zp=int(rng.integers(1, -128, 127)[0]))
+    if pointwise or _pick(rng, [0, 1]):
+        padding = "same"
+    else:
+        pt, pb = _geometry(rng, h, k, stride, dilation)
+        pl, pr = _geometry(rng, w, k, stride, dilation)
+        padding = (pt, pl, pb, pr)
+    lut = _random_lut(p, rng) if _pick(rng, [0, 0, 1]) else None
+    lo = int(rng.integers(1, -24, -1)[0])
+    for shift in ((lo, 3), (-12, -4), (-20, -1), (-24, -16)):
+        try:
+            y = p.conv(x, 16 * int(rng.integers(1, 1, 26)[0]), k=k, stride=stride, dilation=dilation, padding=padding,
+                       act=_pick(rng, ["none", "relu", "relu6"]), q6=int(rng.integers(1, 1, 200)[0]), lut=lut,
+                       shift=shift, w_sigma=_pick(rng, [3, 20, 40]), bias_sigma=_pick(rng, [0, 4096, 60000]))
+            return p.build(y)
+        except ValueError:
+            continue
+    raise AssertionError("unreachable")

@@ -12,8 +12,8 @@ import pytest
 
 import uq_plan as P
 import uq_workloads as W
-from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, dw_mfma_plan, random_plan,
-                       pointwise_wide_plan, rows_conv_plan, stem_plan)
+from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, dw_mfma_plan, gemm_plan,
+                       random_plan, pointwise_wide_plan, rows_conv_plan, stem_plan)
 from test_oracle_vs_reference import (BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, softmax_table_plan,
                                       transpose_plan)
 from refs import oracle_run
@@ -54,12 +54,7 @@ def test_single_image_entry_point(lib):
     _assert_same(Graph(plan, lib).run(x), _oracle(plan, x, 1), "ug_run")
 
 
-@pytest.mark.parametrize("name,images,samples", [("mnv4", 256, (0, 137, 255)), ("yolo", 64, (0, 63)), ("head", 512, (0, 511)),
-                                                 ("conv3x3", 512, (5, 400))])
-def test_full_batch_sampled_images(lib, name, images, samples):
-    plan, _ = W.WORKLOADS[name]()
-    x = P.random_input(plan, images, 33)
-    g = Graph(plan, lib)
+def _run_device(lib, g, x, images):
     din = DeviceBuffer(lib, x.nbytes)
     dout = DeviceBuffer(lib, images * g.output_bytes)
     din.upload(x)
@@ -67,12 +62,62 @@ def test_full_batch_sampled_images(lib, name, images, samples):
     y = dout.download()
     din.free()
     dout.free()
+    return y
+
+
+# Sampled images: the first and last image of the batch, of each image slice
+# (MobileNetV4-S runs as two slices of 128 images) and the images holding the
+# first and last boundary of the GEMM's 256-pixel tiles (head: 49 pixels per
+# image, so tile boundaries fall inside images 5 and 506; conv3x3: 6400
+# pixels per image, whole tiles).
+@pytest.mark.parametrize("name,images,samples", [("mnv4", 256, (0, 127, 128, 255)), ("yolo", 64, (0, 63)),
+                                                 ("head", 512, (0, 5, 255, 256, 506, 511)),
+                                                 ("conv3x3", 512, (0, 1, 256, 511))])
+def test_full_batch_sampled_images(lib, name, images, samples):
+    plan, _ = W.WORKLOADS[name]()
+    x = P.random_input(plan, images, 33)
+    g = Graph(plan, lib)
+    y = _run_device(lib, g, x, images)
     ib, ob = g.input_bytes, g.output_bytes
     for j in samples:
         _assert_same(y[j * ob:(j + 1) * ob], _oracle(plan, x[j * ib:(j + 1) * ib], 1), f"{name} image {j}")
     if name == "mnv4":
-        # Host and device entry points agree on the whole batch.
+        # Host and device entry points agree on the whole batch, and so do
+        # two image slices and one stream.
         _assert_same(g.run_batch(x, images), y, "run_batch vs run_device")
+
+
+@pytest.mark.parametrize("name", ["head", "conv3x3"])
+def test_gemm_whole_batch_matches_conv_kernels(lib, name, monkeypatch):
+    """The large-tile GEMM (which the 512-image launches take) and the
+    16x16x64 conv kernels (UQ_GEMM=0) are independent implementations;
+    they agree on every byte of the batch."""
+    plan, images = W.WORKLOADS[name]()
+    x = P.random_input(plan, images, 34)
+    before = lib.uqk_gemm_launches()
+    y = _run_device(lib, Graph(plan, lib), x, images)
+    assert lib.uqk_gemm_launches() > before, "the large-tile GEMM did not run"
+    monkeypatch.setenv("UQ_GEMM", "0")
+    before = lib.uqk_gemm_launches()
+    y0 = _run_device(lib, Graph(plan, lib), x, images)
+    assert lib.uqk_gemm_launches() == before
+    _assert_same(y, y0, f"{name}: GEMM vs conv kernels")
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_gemm_plans(lib, seed, monkeypatch):
+    """Convs forced onto the large-tile GEMM (all four tile configurations) with pixel,
+    channel and K tails, compared in full with the oracle."""
+    monkeypatch.setenv("UQ_GEMM", "1")
+    monkeypatch.setenv("UQ_GEMM_TILE", str(seed % 4))
+    plan = gemm_plan(9000 + seed)
+    images = 2 + seed % 3
+    x = P.random_input(plan, images, seed)
+    g = Graph(plan, lib)
+    before = lib.uqk_gemm_launches()
+    y = g.run_batch(x, images)
+    assert lib.uqk_gemm_launches() > before, "the large-tile GEMM did not run"
+    _assert_same(y, _oracle(plan, x, images), f"gemm plan {9000 + seed}")
 
 
 @pytest.mark.parametrize("seed", range(80))

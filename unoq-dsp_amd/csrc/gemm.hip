@@ -1,0 +1,440 @@
+// Large-tile int8 convolution GEMM for gfx950 (code 14 layers whose work is
+// matrix-core bound: wide K and many output pixels).
+//
+// The layer is out[p][c] = requant(sum_k s[p][k] * w[c][k]) over the pixels
+// p of the batch (implicit im2col: k = (ky, kx, ic), s = the signed input
+// byte, or the input zero point in padding) and the output channels c; the
+// reference computes the same sum on unsigned columns (qnn.c:1101-1169,
+// gemm.c:592-612), whose +128 offset and K tail the load-time corrected bias
+// absorbs (graph.c: prepare_spatial).
+//
+// Matrix cores: v_mfma_i32_32x32x32_i8, whose measured rate on MI355X is
+// about 1.5x that of v_mfma_i32_16x16x64_i8. The weights are the MFMA rows
+// (A operand) and the pixels its columns, so a lane's accumulator registers
+// 4g .. 4g+3 hold four consecutive channels of one pixel: after
+// requantisation two v_permlane32_swap per 32x32 tile give each lane 16
+// consecutive channels of one pixel, one 16-byte store, with no LDS round
+// trip for the output.
+//
+// Blocking: a block of NWP x NWC waves computes BP = NWP*WP pixels by
+// BC = NWC*WC channels; each wave a WP x WC tile, (WP/32) * (WC/32)
+// accumulators of 16 registers. K advances 64 bytes per stage: the block's
+// pixel rows and weight rows for the stage (BP*64 + BC*64 bytes) are loaded
+// from HBM/L2 with coalesced 16-byte loads into registers, written to one of
+// two LDS buffers while the other buffer feeds the matrix cores, one barrier
+// per stage. A staged row is 64 bytes as four 16-byte chunks, chunk c stored
+// at position c ^ ((row >> 2) & 3): a fragment read (32 consecutive rows,
+// one chunk) and a staging write (four rows, four chunks per 16 lanes) both
+// touch 16 distinct 16-byte bank groups per 16 lanes. Each wave reads its
+// (WP + WC) x 64 bytes per stage from LDS for WP*WC*64 MACs.
+//
+// Block order is XCD-aware: the hardware deals consecutive block ids to the
+// eight XCDs in turn, so block id b is renumbered to put a contiguous range of
+// output tiles (pixel tile major, channel tile minor) on each XCD; a pixel
+// tile's input rows then come from HBM once per XCD and its channel tiles
+// hit that XCD's L2.
+#include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
+#include <stdint.h>
+#include "uqk.h"
+#include "uqk_device.h"
+#include "uqk_internal.h"
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+struct GemmArgs {
+    const int8_t *x;
+    int8_t *y;
+    const int8_t *w;           // [oc_pad][kpad], k = (ky, kx, ic), zero past K
+    const int4 *epi;           // 32-byte requantisation records, one per channel
+    const uint8_t *lut;        // optional post table
+    int M;                     // output pixels of the launch
+    int K, kpad, oc, oc_pad;
+    int ih, iw, ic, ow, ohw, kw, sh, sw, dh, dw, pt, pl;
+    int xz, yz, lo, hi;
+    int ctiles, nblocks;
+};
+
+// Position of logical 16-byte chunk c in staged row `row` of KS bytes (and,
+// XOR being its own inverse, the logical chunk at position c): 64-byte rows
+// as four chunks, c ^ ((row >> 2) & 3); 128-byte rows as eight chunks,
+// c ^ ((row >> 1) & 7). Either way a fragment read (32 consecutive rows, one
+// chunk) touches 16 distinct 16-byte bank groups per 16 lanes.
+template <int KS>
+__device__ __forceinline__ int swz(int row, int c)
+{
+    return KS == 64 ? c ^ ((row >> 2) & 3) : c ^ ((row >> 1) & 7);
+}
+
+// Sixteen bytes of value v at offset 16 * v: the source of staged chunks that
+// hold the input zero point (im2col padding), pixel chunks past K (whose
+// weights are zero, so any finite bytes do) and weight chunks past kpad (row
+// 0: zeros), so that every lane of a staging instruction loads from a valid
+// address.
+struct PadRows {
+    uint8_t b[256 * 16];
+};
+static constexpr PadRows make_pad_rows()
+{
+    PadRows p{};
+    for (int i = 0; i < 256 * 16; i++) p.b[i] = (uint8_t)(i >> 4);
+    return p;
+}
+__device__ const PadRows g_pad_rows = make_pad_rows();
+
+// Sixteen bytes from global memory straight into LDS: lane l's bytes land
+// at LDS address lds + 16 * l (lds wave-uniform). Issued through asm (with
+// no memory clobber) so that the compiler, which would otherwise wait for
+// every outstanding LDS load before each LDS read and barrier, leaves the
+// ring's waits to wait_vm. Order against the LDS reads of the same buffer
+// comes from the barriers: a buffer is refilled only after the barrier that
+// follows its last read, and read only after the wait and barrier that
+// follow its fill. M0 is the LDS base of the instruction.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_load16(const void *src, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds) : "m0");
+}
+#pragma clang diagnostic pop
+
+// Wait until at most N of this wave's vector-memory loads are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// IM2COL: the pixel operand gathered per stage from the input through the
+// (ky, kx, ic) decomposition of k (IC % KS == 0, so a stage lies inside one
+// tap); otherwise pointwise rows of IC bytes. NS: stages in the LDS ring;
+// KS: K bytes per stage (64, or 128 so that every staged row is one whole
+// 128-byte line, which halves the L2 requests per byte).
+template <int WP, int WC, int NWP, int NWC, int NS, int KS, bool IM2COL, int EMODE>
+__global__ __launch_bounds__(64 * NWP * NWC) void k_gemm(GemmArgs a)
+{
+    constexpr int NW = NWP * NWC, T = 64 * NW;
+    constexpr int BP = WP * NWP, BC = WC * NWC;
+    constexpr int PT = WP / 32, CT = WC / 32;
+    constexpr int CPR = KS / 16, RPI = 1024 / KS;       // chunks per row, rows per staging instruction
+    constexpr int NIX = BP / (RPI * NW), NIW = BC / (RPI * NW), NI = NIX + NIW;
+    constexpr int STAGE = (BP + BC) * KS;
+    constexpr bool HI = (EMODE & 1) != 0, CORR = (EMODE & 2) != 0;
+    static_assert(KS == 64 || KS == 128, "stage depth");
+    static_assert(NIX * RPI * NW == BP && NIW * RPI * NW == BC && NW % 2 == 0, "whole staging instructions per wave");
+    static_assert(NS >= 2 && NS <= 6 && (NS - 1) * NI < 64, "stage ring");
+
+    __shared__ __attribute__((aligned(1024))) int8_t ring[NS * STAGE];
+    __shared__ __attribute__((aligned(16))) int r_m[BC], r_t[BC], r_b[BC], r_ls[BC];
+    __shared__ __attribute__((aligned(16))) long long r_c1[BC], r_thr[BC];
+    __shared__ __attribute__((aligned(16))) int8_t lut_s[256];
+
+    const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wp = wave % NWP, wc = wave / NWP;
+    const int nb = a.nblocks, q8 = nb >> 3, r8 = nb & 7, xcd = (int)(blockIdx.x & 7);
+    const int lid = xcd * q8 + min(xcd, r8) + (int)(blockIdx.x >> 3);
+    const int p0 = lid / a.ctiles * BP, c0 = lid % a.ctiles * BC;
+
+    // Requantisation records of the block's channels, one array per field
+    // (channels past OC reuse record 0; their outputs are not stored).
+    for (int j = t; j < BC; j += T) {
+        const int c = c0 + j < a.oc ? c0 + j : 0;
+        const int4 e0 = a.epi[2 * c], e1 = a.epi[2 * c + 1];
+        r_b[j] = e0.x; r_m[j] = e0.y; r_ls[j] = e0.z; r_t[j] = e0.w;
+        r_c1[j] = (long long)(((unsigned long long)(unsigned)e1.y << 32) | (unsigned)e1.x);
+        r_thr[j] = (long long)(((unsigned long long)(unsigned)e1.w << 32) | (unsigned)e1.z);
+    }
+    if (a.lut && t < 64) ((int *)lut_s)[t] = ((const int *)a.lut)[t];
+
+    // Staging: a stage is BP pixel rows then BC weight rows of KS bytes.
+    // Wave w's instruction i fills stage bytes [j * 1024, j * 1024 + 1024)
+    // with j = w + i * NW (instructions 0 .. NIX-1 pixel rows, the rest
+    // weight rows); lane l writes 16 bytes at l * 16, i.e. row
+    // j * RPI + l / CPR, physical chunk l % CPR, so it loads the logical
+    // chunk at that position. The swizzle term depends on row bits that
+    // i * NW * RPI (a multiple of 16) leaves alone, so each thread loads the
+    // same logical chunk cq of all its rows.
+    const int cq = swz<KS>(wave * RPI + lane / CPR, lane % CPR);
+    const int8_t *pad = (const int8_t *)g_pad_rows.b + (a.xz & 0xff) * 16, *zero = (const int8_t *)g_pad_rows.b;
+    const int8_t *xsrc[NIX];
+    int iy0[NIX], ix0[NIX];
+#pragma unroll
+    for (int i = 0; i < NIX; i++) {
+        const int p = min(p0 + (wave + i * NW) * RPI + lane / CPR, a.M - 1);
+        if (IM2COL) {
+            const int n = p / a.ohw, rem = p - n * a.ohw, oy = rem / a.ow, ox = rem - oy * a.ow;
+            iy0[i] = oy * a.sh - a.pt;
+            ix0[i] = ox * a.sw - a.pl;
+            xsrc[i] = a.x + (long)n * a.ih * a.iw * a.ic + ((long)iy0[i] * a.iw + ix0[i]) * a.ic + cq * 16;
+        } else {
+            iy0[i] = ix0[i] = 0;
+            xsrc[i] = a.x + (long)p * a.ic + cq * 16;
+        }
+    }
+    const int8_t *wsrc[NIW];
+#pragma unroll
+    for (int i = 0; i < NIW; i++)
+        wsrc[i] = a.w + (long)min(c0 + (wave + (NIX + i) * NW) * RPI - BP + lane / CPR, a.oc_pad - 1) * a.kpad + cq * 16;
+
+    // Tap state of the next stage to issue (IM2COL): channel offset, kx, ky.
+    int tc = 0, tkx = 0, tky = 0;
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t *)ring;
+    auto issue = [&](int s, int buf) {
+        const int k0 = s * KS;
+        const uint32_t dst = ring_lds + buf * STAGE + wave * 1024;
+        if (IM2COL) {
+            const int dy = tky * a.dh, dx = tkx * a.dw;
+            const long off = ((long)dy * a.iw + dx) * a.ic + tc;
+#pragma unroll
+            for (int i = 0; i < NIX; i++) {
+                const bool in = (unsigned)(iy0[i] + dy) < (unsigned)a.ih && (unsigned)(ix0[i] + dx) < (unsigned)a.iw;
+                lds_load16(in ? xsrc[i] + off : pad, dst + i * NW * 1024);
+            }
+            tc += KS;
+            if (tc == a.ic) {
+                tc = 0;
+                if (++tkx == a.kw) {
+                    tkx = 0;
+                    tky++;
+                }
+            }
+        } else {
+            const bool in = k0 + cq * 16 < a.K;
+#pragma unroll
+            for (int i = 0; i < NIX; i++) lds_load16(in ? xsrc[i] + k0 : pad, dst + i * NW * 1024);
+        }
+        // Weight chunks past kpad (the last stage of a kpad that is not a
+        // multiple of KS) are zero, so the pixel bytes they meet (the
+        // zero-point row) add nothing.
+        const bool win = k0 + cq * 16 < a.kpad;
+#pragma unroll
+        for (int i = 0; i < NIW; i++) lds_load16(win ? wsrc[i] + k0 : zero, dst + (NIX + i) * NW * 1024);
+    };
+
+    v16i acc[CT][PT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+        for (int pt = 0; pt < PT; pt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[ct][pt][r] = 0;
+
+    // Fragments of one 32-byte K half of a staged stage: lane (fr, fh)
+    // takes logical chunk 2h + fh of weight row wc*WC + ct*32 + fr and of
+    // pixel row wp*WP + pt*32 + fr.
+    const int fr = lane & 31, fh = lane >> 5;
+    auto read_frags = [&](int buf, int h, v4i (&wf)[CT], v4i (&xf)[PT]) {
+        const int8_t *xs = ring + buf * STAGE, *ws = xs + BP * KS;
+        const int c = 2 * h + fh;
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++) {
+            const int row = wc * WC + ct * 32 + fr;
+            wf[ct] = *(const v4i *)(ws + row * KS + swz<KS>(row, c) * 16);
+        }
+#pragma unroll
+        for (int pt = 0; pt < PT; pt++) {
+            const int row = wp * WP + pt * 32 + fr;
+            xf[pt] = *(const v4i *)(xs + row * KS + swz<KS>(row, c) * 16);
+        }
+    };
+    auto mfmas = [&](const v4i (&wf)[CT], const v4i (&xf)[PT]) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+            for (int pt = 0; pt < PT; pt++)
+                acc[ct][pt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[ct], xf[pt], acc[ct][pt], 0, 0, 0);
+    };
+    // Wait until this wave's loads of a stage have landed, `later` stages
+    // (0 .. NS-1) having been issued after it.
+    auto wait_stage = [&](int later) {
+        if (later <= 0) wait_vm<0>();
+        else if (later == 1) wait_vm<NI>();
+        else if (later == 2) wait_vm<2 * NI>();
+        else if (later == 3 || NS <= 4) wait_vm<3 * NI>();
+        else if (later == 4 || NS <= 5) wait_vm<(NS > 4 ? 4 : 3) * NI>();
+        else wait_vm<(NS > 5 ? 5 : 3) * NI>();
+    };
+
+    // Software pipeline over stages s = 0 .. S-1 (NS buffers, stage s in
+    // buffer s % NS), each NH = KS / 32 K sub-steps: while the matrix cores
+    // work through sub-step h, sub-step h + 1's fragments come from LDS
+    // (two fragment sets in turn). Before the last sub-step of stage s the
+    // block waits for stage s + 1 (issued NS - 1 stages earlier) and passes
+    // a barrier, after which every wave has read all of stage s, so its
+    // buffer is refilled with stage s + NS while that sub-step multiplies
+    // and stage s + 1's first fragments are read.
+    constexpr int NH = KS / 32;
+    static_assert(NH % 2 == 0, "fragment sets alternate across stages");
+    const int S = (a.kpad + KS - 1) / KS;
+#pragma unroll
+    for (int s = 0; s < NS; s++)
+        if (s < S) issue(s, s);
+    wait_stage(min(NS - 1, S - 1));
+    __syncthreads();
+    v4i wf[2][CT], xf[2][PT];
+    read_frags(0, 0, wf[0], xf[0]);
+    for (int s = 0; s < S; s++) {
+        const int buf = s % NS;
+#pragma unroll
+        for (int h = 0; h < NH; h++) {
+            if (h + 1 < NH) {
+                read_frags(buf, h + 1, wf[(h + 1) & 1], xf[(h + 1) & 1]);
+            } else if (s + 1 < S) {
+                wait_stage(min(NS - 2, S - 2 - s));
+                __syncthreads();
+                if (s + NS < S) issue(s + NS, buf);
+                read_frags((s + 1) % NS, 0, wf[0], xf[0]);
+            }
+            mfmas(wf[h & 1], xf[h & 1]);
+        }
+    }
+
+    // Epilogue: lane (fr, fh) holds, in registers 4g .. 4g+3 of tile
+    // (ct, pt), channels ct*32 + 8g + 4fh + 0..3 of pixel pt*32 + fr.
+    const int vlo = vgpr(a.lo), vhi = vgpr(a.hi);
+    const bool lut = a.lut != nullptr;
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) {
+        int words[PT][4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int cb = wc * WC + ct * 32 + 8 * g + 4 * fh;
+            const int4 m4 = *(const int4 *)&r_m[cb], t4 = *(const int4 *)&r_t[cb];
+            const int4 b4 = *(const int4 *)&r_b[cb], l4 = *(const int4 *)&r_ls[cb];
+            Epi e[4];
+            const int mv[4] = {m4.x, m4.y, m4.z, m4.w}, tv[4] = {t4.x, t4.y, t4.z, t4.w};
+            const int bv[4] = {b4.x, b4.y, b4.z, b4.w}, lv[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                e[i].m = mv[i];
+                e[i].T = tv[i];
+                e[i].bias = bv[i];
+                e[i].ls = lv[i];
+                e[i].c1 = r_c1[cb + i];
+                e[i].cthr = CORR ? r_thr[cb + i] : 0;
+            }
+#pragma unroll
+            for (int pt = 0; pt < PT; pt++) {
+                int v[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[ct][pt][4 * g + i], e[i], a.yz, vlo, vhi);
+                if (lut) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) v[i] = lut_s[v[i] + 128];
+                }
+                words[pt][g] = pack4(v[0], v[1], v[2], v[3]);
+            }
+        }
+        const int cg = c0 + wc * WC + ct * 32 + 16 * fh;
+#pragma unroll
+        for (int pt = 0; pt < PT; pt++) {
+            const auto s02 = __builtin_amdgcn_permlane32_swap(words[pt][0], words[pt][2], false, false);
+            const auto s13 = __builtin_amdgcn_permlane32_swap(words[pt][1], words[pt][3], false, false);
+            const int p = p0 + wp * WP + pt * 32 + fr;
+            if (p < a.M && cg < a.oc)
+                *(v4i *)(a.y + (long)p * a.oc + cg) = (v4i){(int)s02[0], (int)s02[1], (int)s13[0], (int)s13[1]};
+        }
+    }
+}
+
+static uint64_t g_launches;     // successful launches, for tests that must know which kernel ran
+
+// Launches of the large-tile GEMM since the library was loaded (a test hook;
+// not part of the plan ABI).
+extern "C" uint64_t uqk_gemm_launches(void) { return g_launches; }
+
+template <int WP, int WC, int NWP, int NWC, int NS, int KS, bool IM2COL>
+static int launch_gemm(const GemmArgs &a, int emode)
+{
+    hipStream_t st;
+    hipEvent_t e0, e1;
+    uqk_next_launch(&st, &e0, &e1);
+    const dim3 grid((unsigned)a.nblocks), block(64 * NWP * NWC);
+    switch (emode) {
+    case 0: hipExtLaunchKernelGGL((k_gemm<WP, WC, NWP, NWC, NS, KS, IM2COL, 0>), grid, block, 0, st, e0, e1, 0u, a); break;
+    case 1: hipExtLaunchKernelGGL((k_gemm<WP, WC, NWP, NWC, NS, KS, IM2COL, 1>), grid, block, 0, st, e0, e1, 0u, a); break;
+    case 2: hipExtLaunchKernelGGL((k_gemm<WP, WC, NWP, NWC, NS, KS, IM2COL, 2>), grid, block, 0, st, e0, e1, 0u, a); break;
+    default: hipExtLaunchKernelGGL((k_gemm<WP, WC, NWP, NWC, NS, KS, IM2COL, 3>), grid, block, 0, st, e0, e1, 0u, a); break;
+    }
+    const int rc = uqk_fail(hipGetLastError());
+    if (!rc) g_launches++;
+    return rc;
+}
+
+// Tile configurations (pixels x channels per block, waves, LDS stages of K
+// bytes each):
+//   0: 256 x 128, four waves of 128 x 64, three stages of 64 (78 KiB: two blocks per CU)
+//   1: 256 x 256, eight waves of 128 x 64, three stages of 64 (104 KiB)
+//   2: 256 x 128, eight waves of 64 x 64, three stages of 128 (148 KiB)
+//   3: 256 x 256, eight waves of 128 x 64, two stages of 128 (136 KiB)
+static const int g_tile_ks[4] = {64, 64, 128, 128};
+static const int g_tile_bc[4] = {128, 256, 128, 256};
+
+template <bool IM2COL>
+static int launch_tile(int tile, const GemmArgs &a, int emode)
+{
+    switch (tile) {
+    case 1: return launch_gemm<128, 64, 2, 4, 3, 64, IM2COL>(a, emode);
+    case 2: return launch_gemm<64, 64, 4, 2, 3, 128, IM2COL>(a, emode);
+    case 3: return launch_gemm<128, 64, 2, 4, 2, 128, IM2COL>(a, emode);
+    default: return launch_gemm<128, 64, 2, 2, 3, 64, IM2COL>(a, emode);
+    }
+}
+
+static int gemm_im2col(const UQKSpatial *d) { return d->mode == UQK_G16 || d->mode == UQK_ROWS16; }
+
+extern "C" int uqk_gemm_ok(const UQKSpatial *d)
+{
+    if (d->oc % 16 || d->kpad % 64 || d->K < 256) return 0;
+    if (d->mode == UQK_PW) return d->ic % 16 == 0;
+    return gemm_im2col(d) && d->ic % 64 == 0 && d->K == d->kh * d->kw * d->ic && d->kpad == d->K;
+}
+
+// Tile configuration of a launch: 256 x 256 for layers over 128 channels
+// (half the operand traffic per MAC of 256 x 128: 37.5 against 40.2 us for a
+// 1x1 over 960 -> 1280 channels at 25088 pixels), else 256 x 128 with
+// 128-byte stages where an im2col stage stays inside one tap (600 against
+// 628 us for a 3x3 over 128 channels at 3.3M pixels). A forced
+// configuration (d->gemm_tile) whose stages would straddle taps falls back
+// to its 64-byte-stage shape.
+static int gemm_tile(const UQKSpatial *d, uint64_t pixels)
+{
+    (void)pixels;
+    const bool deep_ok = d->mode == UQK_PW || d->ic % 128 == 0;
+    int tile = d->gemm_tile >= 0 ? d->gemm_tile : d->oc > 128 ? 1 : deep_ok ? 2 : 0;
+    if (g_tile_ks[tile] == 128 && !deep_ok) tile -= 2;
+    return tile;
+}
+
+extern "C" int uqk_gemm_take(const UQKSpatial *d, uint64_t pixels)
+{
+    if (d->gemm == 0 || !uqk_gemm_ok(d) || pixels >= 0x7fffffffULL) return 0;
+    if (d->gemm == 1) return 1;
+    return d->K >= 512 && pixels * (uint64_t)d->oc >= (1ULL << 24);
+}
+
+extern "C" int uqk_gemm(const UQKSpatial *d, const void *x, void *y, uint32_t batches)
+{
+    const uint64_t pixels = (uint64_t)batches * d->oh * d->ow;
+    if (!uqk_gemm_ok(d) || !pixels || pixels >= 0x7fffffffULL) return (int)hipErrorInvalidValue;
+    GemmArgs a;
+    a.x = (const int8_t *)x;
+    a.y = (int8_t *)y;
+    a.w = (const int8_t *)d->w;
+    a.epi = (const int4 *)d->epi;
+    a.lut = (const uint8_t *)d->lut;
+    a.M = (int)pixels;
+    a.K = d->K; a.kpad = d->kpad; a.oc = d->oc; a.oc_pad = d->oc_pad;
+    a.ih = d->ih; a.iw = d->iw; a.ic = d->ic; a.ow = d->ow; a.ohw = d->oh * d->ow;
+    a.kw = d->kw; a.sh = d->sh; a.sw = d->sw; a.dh = d->dh; a.dw = d->dw; a.pt = d->pt; a.pl = d->pl;
+    a.xz = d->xz; a.yz = d->yz; a.lo = d->lo; a.hi = d->hi;
+    const int emode = (d->hi_shift ? 1 : 0) | (d->corr ? 2 : 0);
+    const int tile = gemm_tile(d, pixels);
+    const int bp = 256, bc = g_tile_bc[tile];
+    a.ctiles = (d->oc + bc - 1) / bc;
+    const uint64_t blocks = (pixels + bp - 1) / bp * (uint64_t)a.ctiles;
+    if (blocks > 0x7fffffffULL) return (int)hipErrorInvalidValue;
+    a.nblocks = (int)blocks;
+    return d->mode != UQK_PW ? launch_tile<true>(tile, a, emode) : launch_tile<false>(tile, a, emode);
+}

@@ -29,6 +29,8 @@ typedef struct {
     int32_t K, kpad, oc_pad, mode, nt, rb, is_max, vec, corr;
     int32_t hi_shift;          /* every shift in [-22, -1]: records fold bias and zero point into c1 */
     int32_t dwwin;             /* depthwise on tap windows (k_dw_win); wdot holds [ky][wk][C] tap words */
+    int32_t gemm;              /* large-tile GEMM: -1 when the launch is large enough, 0 never, 1 whenever the shape fits */
+    int32_t gemm_tile;         /* its tile configuration: -1 automatic, else 0..3 (gemm.hip) */
     const void *w;
     const void *wdot;
     const void *epi;
@@ -126,6 +128,16 @@ int uqk_graph_launch(void *exec);
 void uqk_graph_destroy(void *exec);
 
 int uqk_conv(const UQKSpatial *d, const void *x, void *y, uint32_t batches);
+
+/* Large-tile conv GEMM (gemm.hip): layers with OC % 16 == 0 and K >= 256
+ * whose A operand is pointwise rows (UQK_PW) or an implicit im2col with
+ * IC % 64 == 0 (UQK_G16 / UQK_ROWS16 weight layouts). uqk_gemm_ok: the
+ * layer's shape fits; uqk_gemm_take: uqk_conv sends a launch of `pixels`
+ * output pixels there (by d->gemm: wide K and many outputs, never, or
+ * always). */
+int uqk_gemm_ok(const UQKSpatial *d);
+int uqk_gemm_take(const UQKSpatial *d, uint64_t pixels);
+int uqk_gemm(const UQKSpatial *d, const void *x, void *y, uint32_t batches);
 
 /* A residual add (op 18) applied in a conv's epilogue: y = add(conv(x), res)
  * (or add(res, conv(x)) when conv_is_a is 0), byte for byte the add op's

@@ -64,6 +64,9 @@ def open_library(path=None):
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    # Test hook outside the plan ABI: launches of the large-tile GEMM.
+    lib.uqk_gemm_launches.restype = C.c_uint64
+    lib.uqk_gemm_launches.argtypes = []
     return lib
 
 
