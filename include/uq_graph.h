@@ -34,8 +34,12 @@ extern "C" {
  *   17 add/mul operands    18 op validation  19 unknown op  20 work > 2e9
  *   21 output undefined    25 v3 lifetime overlap
  *   24 no usable GPU (the reference's "worker unavailable" code)
- * Plans that the reference accepts but that use ops outside the INT8 vision
- * path (float ops, transposes, int8 softmax, mul, bmm) return 19. */
+ * Plans that the reference accepts but that use ops outside the INT8 path
+ * return 19: the float ops (codes 1-4, 7, 8, 11-13) and the u8 x i8 integer
+ * matmuls (6, 9). Every other op code the reference runs loads and runs
+ * here: 5, 10, 14-28 (copy, transpose, conv, depthwise, pool, table
+ * softmax, add, pack, concat, resize, LUT, pad, mean, mul, slice, bmm,
+ * softmax). */
 int ug_load(const void *plan, uint32_t len);
 
 /* graph.h:40, graph.c:438-448. Synchronous single-image run from host memory.
@@ -72,15 +76,24 @@ int ug_run_batch(const void *input, uint64_t ni, void *output, uint64_t no, uint
 
 /* The same on device-resident buffers (pointers from ug_device_alloc or any
  * HIP allocation on the current device). ug_run_device returns when the
- * output is complete; ug_enqueue_device only enqueues on the library stream
- * and ug_synchronize waits for all enqueued work. Between an enqueue and the
- * next synchronize the caller must not free or reuse the buffers. */
+ * output is complete; ug_enqueue_device only enqueues and ug_synchronize
+ * waits for all enqueued work. A batch of at least 128 images runs as two
+ * image slices, one on the library stream and one on a side stream; the side
+ * stream is left unjoined while identical batches (same images, input and
+ * output buffers) follow one another, and any other entry point joins it
+ * before it touches the library stream, results or buffers. Between an
+ * enqueue and the next synchronize the caller must not free or reuse the
+ * buffers. While profiling (ug_profile 1) each profiled batch counts as one
+ * run; its times are added by ug_synchronize, by the next enqueue or by a
+ * counter read. */
 int ug_run_device(const void *d_input, void *d_output, uint32_t images);
 int ug_enqueue_device(const void *d_input, void *d_output, uint32_t images);
 int ug_synchronize(void);
 
 /* All images of a tensor after the last run: bytes = images * tensor bytes
- * (for constants: the tensor bytes). */
+ * (for constants: the tensor bytes). Activation snapshots return 22 once a
+ * caller buffer the last run was bound to has been freed with
+ * ug_device_free. */
 int ug_snapshot_images(uint32_t tensor, void *out, uint64_t bytes);
 
 /* Device buffer helpers for callers without their own HIP allocator. */

@@ -422,3 +422,56 @@ def test_kernel_shape_fuzz(lib, maker, seed):
     images = 2
     x = P.random_input(plan, images, seed)
     _assert_same(Graph(plan, lib).run_batch(x, images), _oracle(plan, x, images), f"{maker.__name__} {seed}")
+
+
+def test_profile_counts_one_run_per_profiled_batch(lib):
+    """ug_profile counters count finished profiled batches: a synchronize
+    with none pending adds nothing; one device run adds one; two enqueues
+    and a synchronize add two, each with its own op times."""
+    plan, _ = W.pointwise()
+    g = Graph(plan, lib)
+    images = 4
+    x = P.random_input(plan, images, 5)
+    din = DeviceBuffer(lib, x.nbytes)
+    dout = DeviceBuffer(lib, images * g.output_bytes)
+    din.upload(x)
+    g.profile(1)
+    assert lib.ug_synchronize() == 0
+    assert g.profile(2)[0] == 0
+    assert lib.ug_run_device(din.ptr, dout.ptr, images) == 0
+    assert lib.ug_synchronize() == 0
+    c = g.profile(2)
+    assert c[0] == 1 and c[1] > 0 and c[2] > 0
+    one = int(c[1])
+    assert lib.ug_enqueue_device(din.ptr, dout.ptr, images) == 0
+    assert lib.ug_enqueue_device(din.ptr, dout.ptr, images) == 0
+    assert lib.ug_synchronize() == 0
+    c = g.profile(2)
+    assert c[0] == 3 and c[1] > one
+    g.profile(0)
+    din.free()
+    dout.free()
+
+
+def test_snapshot_after_freeing_a_bound_buffer(lib):
+    """Once a caller buffer the last run read or wrote is freed, activation
+    snapshots return 22 instead of reading freed memory."""
+    plan = random_plan(1003)
+    g = Graph(plan, lib)
+    images = 3
+    x = P.random_input(plan, images, 6)
+    din = DeviceBuffer(lib, x.nbytes)
+    dout = DeviceBuffer(lib, images * g.output_bytes)
+    din.upload(x)
+    assert lib.ug_run_device(din.ptr, dout.ptr, images) == 0
+    recs = P.tensor_records(plan)
+    inp = struct.unpack_from("<I", plan, 20)[0]
+    buf = np.empty(images * recs[inp][1], np.int8)
+    assert lib.ug_snapshot_images(inp, buf.ctypes.data, buf.nbytes) == 0
+    din.free()
+    assert lib.ug_snapshot_images(inp, buf.ctypes.data, buf.nbytes) == 22
+    assert lib.ug_snapshot(inp, buf.ctypes.data, recs[inp][1]) == 22
+    dout.free()
+    # A new run binds fresh buffers and snapshots work again.
+    assert np.array_equal(g.run_batch(x, images), _oracle(plan, x, images))
+    assert lib.ug_snapshot_images(inp, buf.ctypes.data, buf.nbytes) == 0

@@ -17,7 +17,7 @@ import pytest
 
 import uq_plan as P
 import uq_workloads as W
-from plan_fuzz import random_plan
+from plan_fuzz import ATTENTION_OPS, random_plan
 from refs import ref_plain, ref_release
 from uq_native import open_library
 
@@ -174,3 +174,87 @@ def test_out_of_scope_ops_rejected_with_19(libs):
     prod, ref, C = libs
     assert _load(ref.lib, C, plan) == 0
     assert _load(prod, C, plan) == 19
+
+
+F32 = 1
+
+
+def _f32(p, shape, const=False):
+    t = p.tensor(shape, P.TYPE_I32, np.zeros(int(np.prod(shape)), np.int32) if const else None)
+    p.tensors[t]["type"] = F32
+    return t
+
+
+def _refused_plan(code):
+    """A minimal plan holding op `code` that the reference loader accepts
+    (graph.c:74-104 for codes 1-13)."""
+    p = P.Plan(7)
+    if code in (1, 8):                       # float matmul, plain and packed
+        x = _f32(p, (2, 3))
+        b = _f32(p, (4, 3), const=True)
+        z = _f32(p, (2, 4))
+    elif code in (6, 9):                     # u8 x i8 matmul with correction, plain and packed
+        x = p.tensor((2, 8), P.TYPE_U8)
+        b = p.tensor((4, 8), P.TYPE_I8, np.zeros(32, np.int8))
+        corr = p.tensor((4,), P.TYPE_I32, np.zeros(4, np.int32))
+        z = p.tensor((2, 4), P.TYPE_I32)
+    elif code in (2, 3, 4, 13):              # float elementwise, ReLU, softmax
+        x = _f32(p, (2, 4))
+        b = x
+        z = _f32(p, (2, 4))
+    elif code == 7:                          # int32 -> float cast
+        x = p.tensor((4,), P.TYPE_I32)
+        b = x
+        z = _f32(p, (4,))
+    else:                                    # 11 float im2col, 12 float max pool: 1x1 windows
+        x = _f32(p, (1, 4, 4, 1))
+        b = p.tensor((12,), P.TYPE_I32, np.array([1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 4, 4], np.int32))
+        z = _f32(p, (16, 1)) if code == 11 else _f32(p, (1, 4, 4, 1))
+    p.input_id = x
+    p.zp[x] = 0
+    p._op(code, x, b, z, (3, -2, corr, 1) if code in (6, 9) else (0, 0, 0, 0))
+    return p.build(z)
+
+
+def _header_code_sets():
+    """The op codes include/uq_graph.h calls refused (19) and loaded."""
+    import re
+    from pathlib import Path
+    text = (Path(__file__).resolve().parents[1] / "include" / "uq_graph.h").read_text()
+    text = " ".join(re.sub(r"\n\s*\*(?!/)", " ", text).split())
+
+    def expand(spec):
+        out = set()
+        for part in spec.split(","):
+            part = part.strip()
+            if "-" in part:
+                lo, hi = part.split("-")
+                out |= set(range(int(lo), int(hi) + 1))
+            elif part:
+                out.add(int(part))
+        return out
+    refused = re.search(r"float ops \(codes ([0-9, -]+)\) and the u8 x i8 integer matmuls \(([0-9, ]+)\)", text)
+    loaded = re.search(r"loads and runs here: ([0-9, -]+) \(", text)
+    assert refused and loaded, "header no longer states the op-code sets"
+    return expand(refused.group(1)) | expand(refused.group(2)), expand(loaded.group(1))
+
+
+def test_header_op_code_sets_match_library(libs):
+    """Every code the boundary header calls refused gets 19 on a plan the
+    reference accepts; every code it calls loaded is the library's set, and
+    the two cover the reference's op codes 1-28."""
+    refused, loaded = _header_code_sets()
+    assert refused | loaded == set(range(1, 29)) and not refused & loaded
+    assert loaded == SUPPORTED
+    prod, ref, C = libs
+    for code in sorted(refused):
+        plan = _refused_plan(code)
+        assert _load(ref.lib, C, plan) == 0, f"code {code}: the reference refuses the test plan"
+        assert _load(prod, C, plan) == 19, f"code {code}"
+    # Loaded codes: every one appears in an accepted corpus plan the library
+    # takes (0 with a GPU, 24 without one), never 19.
+    seen = set()
+    for plan in _plans() + [W.yolo()[0]] + [random_plan(7000 + i, ops=ATTENTION_OPS) for i in range(8)]:
+        seen |= _codes(plan)
+        assert _load(prod, C, plan) in (0, 24)
+    assert loaded <= seen, loaded - seen

@@ -72,6 +72,10 @@ static struct {
     Group groups[UG_MAX_OP / 2 + 1];
     uint8_t *pipe_in[2], *pipe_out[2]; /* device chunk buffers of the pipelined batch */
     uint64_t pipe_in_bytes, pipe_out_bytes;
+    /* Activation snapshots unavailable: a caller buffer the last run was
+     * bound to has been freed. Cleared when a run binds pointers anew. */
+    int snap_void;
+    int prof_pending;                    /* a profiled batch is enqueued and its times not yet added */
 } G;
 
 static uint32_t width(uint32_t t) { return t == 1 || t == 4 ? 4 : t == 2 || t == 3 ? 1 : 0; }
@@ -1087,6 +1091,8 @@ static int settle(void)
  * the two streams drift apart and one slice's bandwidth-bound layers overlap
  * the other's latency-bound ones. Anything else settles first (the side
  * stream joins the library stream; uqk_sync waits for both). */
+static int finish_profile(void);
+
 static int enqueue_ops(uint32_t images)
 {
     const int n = slice_count(images);
@@ -1094,6 +1100,12 @@ static int enqueue_ops(uint32_t images)
     uint32_t next = 0;
     if (n == 1) {
         if (settle()) return 24;
+        /* Each profiled batch re-stamps the same per-op events: the one
+         * before it is counted first. */
+        if (G.profile_enabled) {
+            if (finish_profile()) return 24;
+            G.prof_pending = 1;
+        }
         return enqueue_range(0, G.h.no, images, &next);
     }
     const int cont = G.split_open && G.split_n == n && G.split_images == images &&
@@ -1255,6 +1267,7 @@ static int launch_op(uint32_t i, uint32_t images)
 
 static void bind_pointers(const void *d_in, void *d_out)
 {
+    G.snap_void = 0;
     for (uint32_t t = 0; t < G.h.nt; t++) {
         G.ptr[t] = G.ts[t].flags && !G.bcast[t] ? G.dev_arena + G.ts[t].offset : G.act[t];
         G.ext[t] = 0;
@@ -1282,9 +1295,12 @@ static int deliver_output_device(void *d_out, uint32_t images)
     return uqk_d2d(d_out, G.ptr[G.h.output], (size_t)images * t->bytes) ? 24 : 0;
 }
 
+/* Add the per-op times of the pending profiled batch (if any) to the
+ * counters: one run per profiled batch. */
 static int finish_profile(void)
 {
-    if (!G.profile_enabled) return 0;
+    if (!G.profile_enabled || !G.prof_pending) return 0;
+    G.prof_pending = 0;
     if (uqk_sync()) return 24;
     uint64_t total = 0;
     for (uint32_t i = 0; i < G.h.no; i++) {
@@ -1577,7 +1593,7 @@ int ug_snapshot_images(uint32_t index, void *out, uint64_t bytes)
         memcpy(out, G.arena + t->offset, t->bytes);
         return 0;
     }
-    if (!G.last_images || bytes != (uint64_t)G.last_images * t->bytes) return 22;
+    if (G.snap_void || !G.last_images || bytes != (uint64_t)G.last_images * t->bytes) return 22;
     if (settle() || materialize_group(index)) return fail(24);
     if (uqk_d2h(out, G.ptr[index], bytes) || uqk_sync()) return fail(24);
     return 0;
@@ -1591,6 +1607,7 @@ int ug_snapshot(uint32_t index, void *out, uint32_t bytes)
         memcpy(out, G.arena + t->offset, bytes);
         return 0;
     }
+    if (G.snap_void) return 22;
     if (!G.last_images) {
         memcpy(out, G.arena + t->offset, bytes); /* arena contents before any run */
         return 0;
@@ -1603,8 +1620,12 @@ int ug_snapshot(uint32_t index, void *out, uint32_t bytes)
 int ug_profile(uint32_t command, void *out, uint32_t bytes)
 {
     if (!G.ready || command > 2 || !out || (bytes != sizeof(G.ticks) && !(G.h.no <= 128 && bytes == 130 * 8))) return 22;
+    if (command == 2 && finish_profile()) return fail(24);
     if (command == 1) memset(G.ticks, 0, sizeof G.ticks);
-    if (command < 2) G.profile_enabled = (int)command;
+    if (command < 2) {
+        G.profile_enabled = (int)command;
+        G.prof_pending = 0;
+    }
     memcpy(out, G.ticks, bytes);
     return 0;
 }
@@ -1633,6 +1654,14 @@ void *ug_device_alloc(uint64_t bytes)
 int ug_device_free(void *d)
 {
     (void)settle();
+    /* A run bound to this buffer (input, output or an alias of either) can
+     * no longer be snapshotted, and the next batch must not continue its
+     * side stream on it. */
+    if (d && G.ready) {
+        for (uint32_t t = 0; t < G.h.nt; t++)
+            if (G.ext[t] && G.ptr[t] == (uint8_t *)d) G.snap_void = 1;
+        if (G.split_in == d || G.split_out == d) G.split_in = G.split_out = NULL;
+    }
     uqk_free(d);
     return 0;
 }
