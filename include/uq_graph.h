@@ -91,10 +91,26 @@ int ug_enqueue_device(const void *d_input, void *d_output, uint32_t images);
 int ug_synchronize(void);
 
 /* All images of a tensor after the last run: bytes = images * tensor bytes
- * (for constants: the tensor bytes). Activation snapshots return 22 once a
- * caller buffer the last run was bound to has been freed with
- * ug_device_free. */
+ * (for constants: the tensor bytes). Activation snapshots return 22 after a
+ * ug_enqueue_device_noalloc run and once a caller buffer the last run was
+ * bound to has been freed with ug_device_free. */
 int ug_snapshot_images(uint32_t tensor, void *out, uint64_t bytes);
+
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): ug_enqueue_device with every intermediate activation
+ * laid out in the library's static per-GPU scratch (UG_NOALLOC_SCRATCH_BYTES,
+ * 64 MiB, held by each GPU until the process ends) instead of buffers the
+ * library allocates; it calls no allocator. Returns 22 when not loaded, on a
+ * null buffer or zero images, or when the plan's activations for `images`
+ * (each tensor's images * bytes, 256-byte aligned) exceed the scratch; 24 on
+ * a GPU error. Results equal ug_enqueue_device's; ug_synchronize waits for
+ * them. Every call on one GPU uses the same scratch, whose contents the last
+ * call leaves behind: calls that overlap on one GPU (from other threads, or
+ * other streams than the library's) race. Snapshots of activations are not
+ * available after it (22). */
+#define UG_NOALLOC_SCRATCH_BYTES (64u << 20)
+int ug_enqueue_device_noalloc(const void *d_input, void *d_output, uint32_t images);
 
 /* Device buffer helpers for callers without their own HIP allocator. */
 void *ug_device_alloc(uint64_t bytes);

@@ -72,10 +72,13 @@ static struct {
     Group groups[UG_MAX_OP / 2 + 1];
     uint8_t *pipe_in[2], *pipe_out[2]; /* device chunk buffers of the pipelined batch */
     uint64_t pipe_in_bytes, pipe_out_bytes;
-    /* Activation snapshots unavailable: a caller buffer the last run was
-     * bound to has been freed. Cleared when a run binds pointers anew. */
+    /* Activation snapshots unavailable: the last run kept its activations in
+     * the shared scratch (ug_enqueue_device_noalloc), or a caller buffer it
+     * was bound to has been freed. Cleared when a run binds pointers anew. */
     int snap_void;
     int prof_pending;                    /* a profiled batch is enqueued and its times not yet added */
+    uint64_t scratch_generation;         /* generation and images of the scratch layout whose */
+    uint32_t scratch_images;             /* ... per-image constant copies are in place */
 } G;
 
 static uint32_t width(uint32_t t) { return t == 1 || t == 4 ? 4 : t == 2 || t == 3 ? 1 : 0; }
@@ -1358,6 +1361,68 @@ int ug_enqueue_device(const void *d_input, void *d_output, uint32_t images)
     if (G.ptr[G.h.output] != (uint8_t *)d_output && settle()) return fail(24);
     if (deliver_output_device(d_output, images)) return fail(24);
     G.last_images = images;
+    return 0;
+}
+
+/* Tensors that take a scratch slot in a no-allocation run: activations other
+ * than the caller's input (and the caller's output, when the output is an
+ * activation distinct from the input), and constants replicated per image. */
+static int scratch_tensor(uint32_t t)
+{
+    const Tensor *x = G.ts + t;
+    if (x->flags && !G.bcast[t]) return 0;
+    if (t == G.h.input) return 0;
+    if (t == G.h.output && G.h.output != G.h.input && !x->flags) return 0;
+    return 1;
+}
+
+int ug_enqueue_device_noalloc(const void *d_input, void *d_output, uint32_t images)
+{
+    if (!G.ready || !d_input || !d_output || !images) return 22;
+    size_t cap = 0;
+    uint8_t *base = uqk_scratch(&cap);
+    if (!base) return 24;
+    static size_t off[UG_MAX_T];
+    size_t need = 0;
+    for (uint32_t t = 0; t < G.h.nt; t++) {
+        off[t] = 0;
+        if (!scratch_tensor(t)) continue;
+        off[t] = need;
+        need += ((size_t)images * G.ts[t].bytes + 255) & ~(size_t)255;
+        if (need > cap) return 22;
+    }
+    /* Per-image copies of constants in per-image operand slots, made once
+     * per scratch layout; earlier work that may still read the scratch
+     * (the other image slice of the last batch) finishes first. */
+    const int fresh = G.scratch_generation != G.generation || G.scratch_images != images;
+    if (fresh && settle()) return fail(24);
+    G.snap_void = 1;
+    for (uint32_t t = 0; t < G.h.nt; t++) {
+        G.ext[t] = 0;
+        if (scratch_tensor(t)) G.ptr[t] = base + off[t];
+        else G.ptr[t] = G.ts[t].flags ? G.dev_arena + G.ts[t].offset : NULL;
+    }
+    if (fresh) {
+        G.scratch_generation = G.generation;
+        G.scratch_images = 0;
+        for (uint32_t t = 0; t < G.h.nt; t++)
+            if (G.ts[t].flags && G.bcast[t])
+                for (uint32_t k = 0; k < images; k++)
+                    if (uqk_d2d(G.ptr[t] + (size_t)k * G.ts[t].bytes, G.dev_arena + G.ts[t].offset, G.ts[t].bytes))
+                        return fail(24);
+        G.scratch_images = images;
+    }
+    G.ptr[G.h.input] = (uint8_t *)d_input;
+    G.ext[G.h.input] = 1;
+    if (G.h.output != G.h.input && !G.ts[G.h.output].flags) {
+        G.ptr[G.h.output] = (uint8_t *)d_output;
+        G.ext[G.h.output] = 1;
+    }
+    if (enqueue_ops(images)) return fail(24);
+    if (G.ptr[G.h.output] != (uint8_t *)d_output && settle()) return fail(24);
+    if (deliver_output_device(d_output, images)) return fail(24);
+    G.last_images = 0;
+    for (uint32_t g = 0; g < G.ngroups; g++) G.groups[g].last_images = 0;
     return 0;
 }
 

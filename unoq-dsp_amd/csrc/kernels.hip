@@ -2839,12 +2839,37 @@ extern "C" int uqk_device_count(void)
     return n;
 }
 
+// Scratch of the no-allocation entry point (ug_enqueue_device_noalloc in
+// graph.c): the intermediate activations of one call, laid out by graph.c.
+// Each GPU holds its own copy of the array, at its own address, until the
+// process ends. In host code the array's name is only a stand-in for the
+// device symbol: its device address comes from hipGetSymbolAddress at init,
+// with the device current, and host code uses that address only.
+#define UQK_MAX_DEVICES 64
+static __device__ __align__(256) uint8_t scratch[UQK_SCRATCH_BYTES];
+static void *g_scratch[UQK_MAX_DEVICES];
+static int g_device;
+
+extern "C" void *uqk_scratch(size_t *bytes)
+{
+    if (!g_ready) return nullptr;
+    if (bytes) *bytes = UQK_SCRATCH_BYTES;
+    return g_scratch[g_device];
+}
+
 extern "C" int uqk_init(void)
 {
     if (g_ready) return 0;
     int n = 0;
     UQK_TRY(hipGetDeviceCount(&n));
     if (n < 1) return (int)hipErrorNoDevice;
+    UQK_TRY(hipGetDevice(&g_device));
+    if (g_device < 0 || g_device >= UQK_MAX_DEVICES) return (int)hipErrorInvalidDevice;
+    if (!g_scratch[g_device]) {
+        void *p = nullptr;
+        UQK_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        g_scratch[g_device] = p;
+    }
     // All streams at the default priority.
     UQK_TRY(hipStreamCreateWithFlags(&g_main, hipStreamNonBlocking));
     g_stream = g_main;

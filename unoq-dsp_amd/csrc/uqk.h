@@ -85,6 +85,11 @@ int uqk_conv_rows_ok(const UQKSpatial *d);
 
 int uqk_init(void);
 int uqk_device_count(void);
+/* The no-allocation entry point's device scratch: a static array of
+ * UQK_SCRATCH_BYTES per GPU, 256-byte aligned; its address on the device
+ * that was current at uqk_init (NULL before it). */
+#define UQK_SCRATCH_BYTES (64u << 20)
+void *uqk_scratch(size_t *bytes);
 void *uqk_malloc(size_t bytes);
 void uqk_free(void *p);
 int uqk_h2d(void *dst, const void *src, size_t bytes);        /* async on the stream */

@@ -27,6 +27,7 @@ SIGNATURES = [
     ("ug_run_batch", C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64, C.c_uint32]),
     ("ug_run_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32]),
     ("ug_enqueue_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32]),
+    ("ug_enqueue_device_noalloc", C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32]),
     ("ug_synchronize", C.c_int, []),
     ("ug_snapshot_images", C.c_int, [C.c_uint32, C.c_void_p, C.c_uint64]),
     ("ug_device_alloc", C.c_void_p, [C.c_uint64]),
