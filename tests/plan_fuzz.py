@@ -388,3 +388,33 @@ def gemm_plan(seed):
         except ValueError:
             continue
     raise AssertionError("unreachable")
+
+
+def gemm_rows_plan(seed):
+    """A conv the row-staged GEMM takes: 128 input channels, stride 1, no
+    dilation, 3x3 / 5x5 / 1x3 / 3x1 kernels, SAME or explicit padding, up to
+    128 output channels in steps of 16, maps from 3x3 to 80 columns (tiles
+    of 512 pixels that start mid-row and end short of it), post tables,
+    activations and all requantisation ranges."""
+    rng = Rng(seed, 575757)
+    p = Plan(seed)
+    h, w = _pick(rng, [(3, 3), (7, 7), (9, 13), (20, 11), (24, 80), (33, 40), (5, 64)])
+    x = p.input((1, h, w, 128), zp=int(rng.integers(1, -128, 127)[0]))
+    kh, kw = _pick(rng, [(3, 3), (3, 3), (5, 5), (1, 3), (3, 1)])
+    if _pick(rng, [0, 1]):
+        padding = "same"
+    else:
+        pt, pb = _geometry(rng, h, kh, 1, 1)
+        pl, pr = _geometry(rng, w, kw, 1, 1)
+        padding = (pt, pl, pb, pr)
+    lut = _random_lut(p, rng) if _pick(rng, [0, 0, 1]) else None
+    lo = int(rng.integers(1, -24, -1)[0])
+    for shift in ((lo, 3), (-12, -4), (-20, -1), (-24, -16)):
+        try:
+            y = p.conv(x, 16 * int(rng.integers(1, 1, 8)[0]), k=kh, kw=kw, padding=padding,
+                       act=_pick(rng, ["none", "relu", "relu6"]), q6=int(rng.integers(1, 1, 200)[0]), lut=lut,
+                       shift=shift, w_sigma=_pick(rng, [3, 20, 40]), bias_sigma=_pick(rng, [0, 4096, 60000]))
+            return p.build(y)
+        except ValueError:
+            continue
+    raise AssertionError("unreachable")

@@ -13,7 +13,7 @@ import pytest
 import uq_plan as P
 import uq_workloads as W
 from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, dw_mfma_plan, gemm_plan,
-                       random_plan, pointwise_wide_plan, rows_conv_plan, stem_plan)
+                       gemm_rows_plan, random_plan, pointwise_wide_plan, rows_conv_plan, stem_plan)
 from test_oracle_vs_reference import (BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, softmax_table_plan,
                                       transpose_plan)
 from refs import oracle_run
@@ -102,6 +102,23 @@ def test_gemm_whole_batch_matches_conv_kernels(lib, name, monkeypatch):
     y0 = _run_device(lib, Graph(plan, lib), x, images)
     assert lib.uqk_gemm_launches() == before
     _assert_same(y, y0, f"{name}: GEMM vs conv kernels")
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_gemm_rows_plans(lib, seed, monkeypatch):
+    """Convs on the row-staged GEMM (persistent blocks over 512-pixel tiles
+    of staged input rows), several images per batch, compared in full with
+    the oracle."""
+    monkeypatch.setenv("UQ_GEMM", "1")
+    monkeypatch.setenv("UQ_GEMM_TILE", "4")
+    plan = gemm_rows_plan(9500 + seed)
+    images = 1 + seed % 4
+    x = P.random_input(plan, images, seed)
+    g = Graph(plan, lib)
+    before = lib.uqk_gemm_launches()
+    y = g.run_batch(x, images)
+    assert lib.uqk_gemm_launches() > before, "the GEMM did not run"
+    _assert_same(y, _oracle(plan, x, images), f"gemm rows plan {9500 + seed}")
 
 
 @pytest.mark.parametrize("seed", range(48))

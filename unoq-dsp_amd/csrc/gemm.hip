@@ -53,6 +53,7 @@ struct GemmArgs {
     int ih, iw, ic, ow, ohw, kw, sh, sw, dh, dw, pt, pl;
     int xz, yz, lo, hi;
     int ctiles, nblocks;
+    int rotate;                // start each block's K walk at a different stage
 };
 
 // Position of logical 16-byte chunk c in staged row `row` of KS bytes (and,
@@ -89,12 +90,13 @@ __device__ const PadRows g_pad_rows = make_pad_rows();
 // ring's waits to wait_vm. Order against the LDS reads of the same buffer
 // comes from the barriers: a buffer is refilled only after the barrier that
 // follows its last read, and read only after the wait and barrier that
-// follow its fill. M0 is the LDS base of the instruction.
+// follow its fill. M0 is the LDS base of the instruction (one wait state
+// between writing M0 and the load that reads it).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_load16(const void *src, uint32_t lds)
 {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds) : "m0");
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds) : "m0");
 }
 #pragma clang diagnostic pop
 
@@ -104,6 +106,84 @@ __device__ __forceinline__ void wait_vm()
 {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// Requantisation records of a block's channels in LDS, one array per field.
+struct EpiLds {
+    int *m, *t, *b, *ls;
+    long long *c1, *thr;
+};
+
+// Load records of channels c0 .. c0 + n - 1 (channels past OC reuse record
+// 0; their outputs are not stored) into the LDS arrays, threads t, t + T, ...
+template <int T>
+__device__ __forceinline__ void load_records(const EpiLds &r, const int4 *epi, int c0, int n, int oc, int t)
+{
+    for (int j = t; j < n; j += T) {
+        const int c = c0 + j < oc ? c0 + j : 0;
+        const int4 e0 = epi[2 * c], e1 = epi[2 * c + 1];
+        r.b[j] = e0.x; r.m[j] = e0.y; r.ls[j] = e0.z; r.t[j] = e0.w;
+        r.c1[j] = (long long)(((unsigned long long)(unsigned)e1.y << 32) | (unsigned)e1.x);
+        r.thr[j] = (long long)(((unsigned long long)(unsigned)e1.w << 32) | (unsigned)e1.z);
+    }
+}
+
+// Requantise and store a wave's tile: lane (fr, fh) holds, in registers
+// 4g .. 4g+3 of accumulator (ct, pt), channels ct*32 + 8g + 4fh + 0..3 of
+// pixel pt*32 + fr (channels local to the block from cb, global from cg;
+// pixel rows of the output from prow). Four channel words per pixel go
+// through two v_permlane32_swap so that each lane stores 16 consecutive
+// channels of one pixel. Rows at or past plimit and channels at or past OC
+// (a multiple of 16) are not stored.
+template <int PT, int CT, bool HI, bool CORR>
+__device__ __forceinline__ void gemm_store(const v16i (&acc)[CT][PT], const EpiLds &r, const int8_t *lut_s, bool lut,
+                                           int8_t *y, int oc, int yz, int lo, int hi, int cb, int cg, long prow,
+                                           long plimit, int lane)
+{
+    const int fr = lane & 31, fh = lane >> 5;
+    const int vlo = vgpr(lo), vhi = vgpr(hi);
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) {
+        int words[PT][4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int c = cb + ct * 32 + 8 * g + 4 * fh;
+            const int4 m4 = *(const int4 *)&r.m[c], t4 = *(const int4 *)&r.t[c];
+            const int4 b4 = *(const int4 *)&r.b[c], l4 = *(const int4 *)&r.ls[c];
+            Epi e[4];
+            const int mv[4] = {m4.x, m4.y, m4.z, m4.w}, tv[4] = {t4.x, t4.y, t4.z, t4.w};
+            const int bv[4] = {b4.x, b4.y, b4.z, b4.w}, lv[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                e[i].m = mv[i];
+                e[i].T = tv[i];
+                e[i].bias = bv[i];
+                e[i].ls = lv[i];
+                e[i].c1 = r.c1[c + i];
+                e[i].cthr = CORR ? r.thr[c + i] : 0;
+            }
+#pragma unroll
+            for (int pt = 0; pt < PT; pt++) {
+                int v[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[ct][pt][4 * g + i], e[i], yz, vlo, vhi);
+                if (lut) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) v[i] = lut_s[v[i] + 128];
+                }
+                words[pt][g] = pack4(v[0], v[1], v[2], v[3]);
+            }
+        }
+        const int cgl = cg + ct * 32 + 16 * fh;
+#pragma unroll
+        for (int pt = 0; pt < PT; pt++) {
+            const auto s02 = __builtin_amdgcn_permlane32_swap(words[pt][0], words[pt][2], false, false);
+            const auto s13 = __builtin_amdgcn_permlane32_swap(words[pt][1], words[pt][3], false, false);
+            const long p = prow + pt * 32 + fr;
+            if (p < plimit && cgl < oc)
+                *(v4i *)(y + p * oc + cgl) = (v4i){(int)s02[0], (int)s02[1], (int)s13[0], (int)s13[1]};
+        }
+    }
 }
 
 // IM2COL: the pixel operand gathered per stage from the input through the
@@ -136,15 +216,8 @@ __global__ __launch_bounds__(64 * NWP * NWC) void k_gemm(GemmArgs a)
     const int lid = xcd * q8 + min(xcd, r8) + (int)(blockIdx.x >> 3);
     const int p0 = lid / a.ctiles * BP, c0 = lid % a.ctiles * BC;
 
-    // Requantisation records of the block's channels, one array per field
-    // (channels past OC reuse record 0; their outputs are not stored).
-    for (int j = t; j < BC; j += T) {
-        const int c = c0 + j < a.oc ? c0 + j : 0;
-        const int4 e0 = a.epi[2 * c], e1 = a.epi[2 * c + 1];
-        r_b[j] = e0.x; r_m[j] = e0.y; r_ls[j] = e0.z; r_t[j] = e0.w;
-        r_c1[j] = (long long)(((unsigned long long)(unsigned)e1.y << 32) | (unsigned)e1.x);
-        r_thr[j] = (long long)(((unsigned long long)(unsigned)e1.w << 32) | (unsigned)e1.z);
-    }
+    const EpiLds recs = {r_m, r_t, r_b, r_ls, r_c1, r_thr};
+    load_records<T>(recs, a.epi, c0, BC, a.oc, t);
     if (a.lut && t < 64) ((int *)lut_s)[t] = ((const int *)a.lut)[t];
 
     // Staging: a stage is BP pixel rows then BC weight rows of KS bytes.
@@ -177,27 +250,26 @@ __global__ __launch_bounds__(64 * NWP * NWC) void k_gemm(GemmArgs a)
     for (int i = 0; i < NIW; i++)
         wsrc[i] = a.w + (long)min(c0 + (wave + (NIX + i) * NW) * RPI - BP + lane / CPR, a.oc_pad - 1) * a.kpad + cq * 16;
 
-    // Tap state of the next stage to issue (IM2COL): channel offset, kx, ky.
-    int tc = 0, tkx = 0, tky = 0;
+    // The block's walk over the S stages of K starts at stage `rot` (the sum
+    // does not depend on the order): blocks that run side by side then read
+    // different weight and pixel lines at any one time instead of all
+    // requesting the same lines of L2 together.
+    const int S = (a.kpad + KS - 1) / KS;
+    const int rot = a.rotate ? lid % S : 0;
     const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t *)ring;
     auto issue = [&](int s, int buf) {
-        const int k0 = s * KS;
+        const int ks = s + rot < S ? s + rot : s + rot - S;
+        const int k0 = ks * KS;
         const uint32_t dst = ring_lds + buf * STAGE + wave * 1024;
         if (IM2COL) {
+            const int tap = k0 / a.ic, tc = k0 - tap * a.ic;
+            const int tky = tap / a.kw, tkx = tap - tky * a.kw;
             const int dy = tky * a.dh, dx = tkx * a.dw;
             const long off = ((long)dy * a.iw + dx) * a.ic + tc;
 #pragma unroll
             for (int i = 0; i < NIX; i++) {
                 const bool in = (unsigned)(iy0[i] + dy) < (unsigned)a.ih && (unsigned)(ix0[i] + dx) < (unsigned)a.iw;
                 lds_load16(in ? xsrc[i] + off : pad, dst + i * NW * 1024);
-            }
-            tc += KS;
-            if (tc == a.ic) {
-                tc = 0;
-                if (++tkx == a.kw) {
-                    tkx = 0;
-                    tky++;
-                }
             }
         } else {
             const bool in = k0 + cq * 16 < a.K;
@@ -266,7 +338,6 @@ __global__ __launch_bounds__(64 * NWP * NWC) void k_gemm(GemmArgs a)
     // and stage s + 1's first fragments are read.
     constexpr int NH = KS / 32;
     static_assert(NH % 2 == 0, "fragment sets alternate across stages");
-    const int S = (a.kpad + KS - 1) / KS;
 #pragma unroll
     for (int s = 0; s < NS; s++)
         if (s < S) issue(s, s);
@@ -290,51 +361,210 @@ __global__ __launch_bounds__(64 * NWP * NWC) void k_gemm(GemmArgs a)
         }
     }
 
-    // Epilogue: lane (fr, fh) holds, in registers 4g .. 4g+3 of tile
-    // (ct, pt), channels ct*32 + 8g + 4fh + 0..3 of pixel pt*32 + fr.
-    const int vlo = vgpr(a.lo), vhi = vgpr(a.hi);
-    const bool lut = a.lut != nullptr;
+    gemm_store<PT, CT, HI, CORR>(acc, recs, lut_s, a.lut != nullptr, a.y, a.oc, a.yz, a.lo, a.hi, wc * WC,
+                                 c0 + wc * WC, (long)p0 + wp * WP, a.M, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Row-staged implicit GEMM for stride-1, undilated convs over exactly 128
+// input channels with at most 128 output channels (3x3 over 128 channels at
+// 80x80, for instance): the im2col kernel above stages every tap's pixel rows
+// again (nine times the input for a 3x3) and re-streams all weights for each
+// 256-pixel tile. Here a block owns 512 consecutive output pixels of one
+// image at a time (a tile) and stages the input rows those pixels touch, with
+// the kernel's halo and padding (the zero point) around them, once per tile
+// in LDS; each tap then reads its shifted window of those rows. The weights
+// of one tap (128 channels x 128 bytes) stream through a three-stage ring.
+// Blocks are persistent, one per CU, over a contiguous range of tiles: once
+// a tile's last stage is read, the next tile's input rows and first weight
+// stage are issued before the tile's epilogue runs, so that staging overlaps
+// requantisation.
+struct RowsArgs {
+    const int8_t *x;
+    int8_t *y;
+    const int8_t *w;           // [oc_pad][kpad], k = (ky, kx, ic), kpad = kh * kw * 128
+    const int4 *epi;
+    const uint8_t *lut;
+    int ih, iw, ow, ohw, kh, kw, pt, pl, oc, oc_pad, kpad, xz, yz, lo, hi;
+    int cols;                  // staged columns: ow + kw - 1
+    int tiles_per_image, tiles;
+};
+
+constexpr int RG_BP = 512, RG_BC = 128, RG_NS = 3, RG_NW = 8;
+constexpr int RG_SLOTS = 832;                          // staged pixels (128 bytes each) per tile
+constexpr int RG_NIN = RG_SLOTS / (8 * RG_NW);         // input staging instructions per wave
+constexpr int RG_NIW = RG_BC * 128 / 1024 / RG_NW;     // weight instructions per wave per stage
+static_assert(RG_NIN * 8 * RG_NW == RG_SLOTS, "whole staging instructions");
+
+template <int EMODE>
+__global__ __launch_bounds__(64 * RG_NW) void k_gemm_rows(RowsArgs a)
+{
+    constexpr int KS = 128, WP = 128, WC = 64, NWP = 4, NW = RG_NW, T = 64 * NW;
+    constexpr int PT = WP / 32, CT = WC / 32, NS = RG_NS, NIW = RG_NIW, NH = KS / 32;
+    constexpr int WSTAGE = RG_BC * KS;
+    constexpr bool HI = (EMODE & 1) != 0, CORR = (EMODE & 2) != 0;
+
+    __shared__ __attribute__((aligned(1024))) int8_t xin[RG_SLOTS * 128];
+    __shared__ __attribute__((aligned(1024))) int8_t ring[NS * WSTAGE];
+    __shared__ __attribute__((aligned(16))) int r_m[RG_BC], r_t[RG_BC], r_b[RG_BC], r_ls[RG_BC];
+    __shared__ __attribute__((aligned(16))) long long r_c1[RG_BC], r_thr[RG_BC];
+    __shared__ __attribute__((aligned(16))) int8_t lut_s[256];
+
+    const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wp = wave % NWP, wc = wave / NWP;
+    const int fr = lane & 31, fh = lane >> 5;
+    const int per = a.tiles / (int)gridDim.x, extra = a.tiles % (int)gridDim.x, b = (int)blockIdx.x;
+    const int t_begin = b * per + min(b, extra), t_end = t_begin + per + (b < extra ? 1 : 0);
+    if (t_begin >= t_end) return;
+
+    const EpiLds recs = {r_m, r_t, r_b, r_ls, r_c1, r_thr};
+    load_records<T>(recs, a.epi, 0, RG_BC, a.oc, t);
+    if (a.lut && t < 64) ((int *)lut_s)[t] = ((const int *)a.lut)[t];
+
+    const int8_t *pad = (const int8_t *)g_pad_rows.b + (a.xz & 0xff) * 16;
+    const uint32_t xin_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t *)xin;
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t *)ring;
+    const int S = a.kh * a.kw;
+
+    // Weight rows of the ring: instruction i of wave w fills rows
+    // (w + i * NW) * 8 + lane / 8; the chunk a lane loads is the same for
+    // all i (swizzle bits unchanged by i * NW * 8).
+    const int cqw = swz<KS>(wave * 8 + lane / 8, lane % 8);
+    const int8_t *wsrc[NIW];
 #pragma unroll
-    for (int ct = 0; ct < CT; ct++) {
-        int words[PT][4];
+    for (int i = 0; i < NIW; i++)
+        wsrc[i] = a.w + (long)min((wave + i * NW) * 8 + lane / 8, a.oc_pad - 1) * a.kpad + cqw * 16;
+    auto issue_w = [&](int s, int buf) {
+        const uint32_t dst = ring_lds + buf * WSTAGE + wave * 1024;
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const int cb = wc * WC + ct * 32 + 8 * g + 4 * fh;
-            const int4 m4 = *(const int4 *)&r_m[cb], t4 = *(const int4 *)&r_t[cb];
-            const int4 b4 = *(const int4 *)&r_b[cb], l4 = *(const int4 *)&r_ls[cb];
-            Epi e[4];
-            const int mv[4] = {m4.x, m4.y, m4.z, m4.w}, tv[4] = {t4.x, t4.y, t4.z, t4.w};
-            const int bv[4] = {b4.x, b4.y, b4.z, b4.w}, lv[4] = {l4.x, l4.y, l4.z, l4.w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                e[i].m = mv[i];
-                e[i].T = tv[i];
-                e[i].bias = bv[i];
-                e[i].ls = lv[i];
-                e[i].c1 = r_c1[cb + i];
-                e[i].cthr = CORR ? r_thr[cb + i] : 0;
-            }
-#pragma unroll
-            for (int pt = 0; pt < PT; pt++) {
-                int v[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) v[i] = conv_requant<HI, CORR>(acc[ct][pt][4 * g + i], e[i], a.yz, vlo, vhi);
-                if (lut) {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) v[i] = lut_s[v[i] + 128];
-                }
-                words[pt][g] = pack4(v[0], v[1], v[2], v[3]);
+        for (int i = 0; i < NIW; i++) lds_load16(wsrc[i] + s * KS, dst + i * NW * 1024);
+    };
+    // Tile geometry: image n, output pixels [pbeg, pend) of it, first output
+    // row oy_a, staged rows (output rows spanned plus the kernel's halo).
+    struct Tile {
+        int n, pbeg, pend, oy_a, rows;
+    };
+    auto geom = [&](int tile) {
+        Tile g;
+        g.n = tile / a.tiles_per_image;
+        g.pbeg = (tile - g.n * a.tiles_per_image) * RG_BP;
+        g.pend = min(g.pbeg + RG_BP, a.ohw);
+        g.oy_a = g.pbeg / a.ow;
+        g.rows = (g.pend - 1) / a.ow - g.oy_a + a.kh;
+        return g;
+    };
+    // Staged slot q = staged row r * cols + column c holds input pixel
+    // (oy_a - pt + r, c - pl), or the zero point outside the image (and past
+    // the tile's rows); its 16-byte chunks are swizzled by q as ring rows are.
+    auto issue_in = [&](const Tile &g) {
+        const int8_t *img = a.x + (long)g.n * a.ih * a.iw * 128;
+        const int iyb = g.oy_a - a.pt;
+        // Slots q, q + 64, ... of this lane (instruction i adds NW * 8), with
+        // their staged row and column stepped along.
+        int q = wave * 8 + lane / 8;
+        int r = q / a.cols, c = q - r * a.cols;
+#pragma unroll 1
+        for (int i = 0; i < RG_NIN; i++) {
+            const int iy = iyb + r, ix = c - a.pl;
+            const int cq = swz<KS>(q, lane % 8);
+            const bool in = r < g.rows && (unsigned)iy < (unsigned)a.ih && (unsigned)ix < (unsigned)a.iw;
+            lds_load16(in ? img + ((long)iy * a.iw + ix) * 128 + cq * 16 : pad, xin_lds + (wave + i * NW) * 1024);
+            q += NW * 8;
+            c += NW * 8;
+            while (c >= a.cols) {
+                c -= a.cols;
+                r++;
             }
         }
-        const int cg = c0 + wc * WC + ct * 32 + 16 * fh;
+    };
+
+    v16i acc[CT][PT];
+    int qb[PT];
+    auto read_frags = [&](int s, int h, v4i (&wf)[CT], v4i (&xf)[PT]) {
+        const int ky = s / a.kw, kx = s - ky * a.kw, toff = ky * a.cols + kx;
+        const int c = 2 * h + fh;
+        const int8_t *ws = ring + (s % NS) * WSTAGE;
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++) {
+            const int row = wc * WC + ct * 32 + fr;
+            wf[ct] = *(const v4i *)(ws + row * KS + swz<KS>(row, c) * 16);
+        }
 #pragma unroll
         for (int pt = 0; pt < PT; pt++) {
-            const auto s02 = __builtin_amdgcn_permlane32_swap(words[pt][0], words[pt][2], false, false);
-            const auto s13 = __builtin_amdgcn_permlane32_swap(words[pt][1], words[pt][3], false, false);
-            const int p = p0 + wp * WP + pt * 32 + fr;
-            if (p < a.M && cg < a.oc)
-                *(v4i *)(a.y + (long)p * a.oc + cg) = (v4i){(int)s02[0], (int)s02[1], (int)s13[0], (int)s13[1]};
+            const int q = qb[pt] + toff;
+            xf[pt] = *(const v4i *)(xin + q * KS + swz<KS>(q, c) * 16);
         }
+    };
+    auto mfmas = [&](const v4i (&wf)[CT], const v4i (&xf)[PT]) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+            for (int pt = 0; pt < PT; pt++)
+                acc[ct][pt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[ct], xf[pt], acc[ct][pt], 0, 0, 0);
+    };
+    auto wait_stage = [&](int later) {
+        if (later <= 0) wait_vm<0>();
+        else if (later == 1) wait_vm<NIW>();
+        else wait_vm<2 * NIW>();
+    };
+
+    // Load order per tile: input rows, weight stage 0, (the previous tile's
+    // stores), weight stages 1 .. NS-1; the first wait then leaves only
+    // stages 1 .. NS-1 outstanding.
+    Tile g = geom(t_begin);
+    issue_in(g);
+#pragma unroll
+    for (int s = 0; s < NS; s++)
+        if (s < S) issue_w(s, s);
+    for (int tile = t_begin;;) {
+#pragma unroll
+        for (int pt = 0; pt < PT; pt++) {
+            const int o = min(g.pbeg + wp * WP + pt * 32 + fr, g.pend - 1);
+            const int oy = o / a.ow, ox = o - oy * a.ow;
+            qb[pt] = (oy - g.oy_a) * a.cols + ox;
+        }
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+            for (int pt = 0; pt < PT; pt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[ct][pt][r] = 0;
+        wait_stage(min(NS - 1, S - 1));
+        __syncthreads();
+        v4i wf[2][CT], xf[2][PT];
+        read_frags(0, 0, wf[0], xf[0]);
+        for (int s = 0; s < S; s++) {
+#pragma unroll
+            for (int h = 0; h < NH; h++) {
+                if (h + 1 < NH) {
+                    read_frags(s, h + 1, wf[(h + 1) & 1], xf[(h + 1) & 1]);
+                } else if (s + 1 < S) {
+                    wait_stage(min(NS - 2, S - 2 - s));
+                    __syncthreads();
+                    if (s + NS < S) issue_w(s + NS, s % NS);
+                    read_frags(s + 1, 0, wf[0], xf[0]);
+                }
+                mfmas(wf[h & 1], xf[h & 1]);
+            }
+        }
+        // Every wave has read the tile's rows and its last stages: the next
+        // tile's rows and first stage go in before this tile's epilogue.
+        __syncthreads();
+        const Tile cur = g;
+        const int next = tile + 1;
+        if (next < t_end) {
+            g = geom(next);
+            issue_in(g);
+            issue_w(0, 0);
+        }
+        const long prow = (long)cur.n * a.ohw;
+        gemm_store<PT, CT, HI, CORR>(acc, recs, lut_s, a.lut != nullptr, a.y, a.oc, a.yz, a.lo, a.hi, wc * WC,
+                                     wc * WC, prow + cur.pbeg + wp * WP, prow + cur.pend, lane);
+        if (next >= t_end) break;
+#pragma unroll
+        for (int s = 1; s < NS; s++)
+            if (s < S) issue_w(s, s);
+        tile = next;
     }
 }
 
@@ -368,6 +598,7 @@ static int launch_gemm(const GemmArgs &a, int emode)
 //   1: 256 x 256, eight waves of 128 x 64, three stages of 64 (104 KiB)
 //   2: 256 x 128, eight waves of 64 x 64, three stages of 128 (148 KiB)
 //   3: 256 x 256, eight waves of 128 x 64, two stages of 128 (136 KiB)
+//   4: the row-staged kernel (k_gemm_rows), where the layer fits it
 static const int g_tile_ks[4] = {64, 64, 128, 128};
 static const int g_tile_bc[4] = {128, 256, 128, 256};
 
@@ -383,6 +614,63 @@ static int launch_tile(int tile, const GemmArgs &a, int emode)
 }
 
 static int gemm_im2col(const UQKSpatial *d) { return d->mode == UQK_G16 || d->mode == UQK_ROWS16; }
+
+// Whether a layer fits the row-staged kernel: stride 1, no dilation, 128
+// input channels (one 128-byte stage per tap), at most 128 output channels,
+// at least three taps, and the rows that 512 consecutive output pixels of one
+// image touch (plus the kernel's halo) within the staged slots. *cols: staged
+// columns.
+static int rows_fit(const UQKSpatial *d, int *cols)
+{
+    if (!gemm_im2col(d) || d->ic != 128 || d->sh != 1 || d->sw != 1 || d->dh != 1 || d->dw != 1) return 0;
+    if (d->oc > RG_BC || d->oc % 16 || d->K != d->kh * d->kw * 128 || d->kpad != d->K || d->kh * d->kw < 3) return 0;
+    const long c = (long)d->ow + d->kw - 1;
+    long span = (RG_BP - 1 + d->ow - 1) / d->ow + 1;
+    if (span > d->oh) span = d->oh;           /* a tile never leaves its image */
+    if ((span + d->kh - 1) * c > RG_SLOTS) return 0;
+    *cols = (int)c;
+    return 1;
+}
+
+static int g_cus;               // compute units of the device (persistent grid size)
+
+static int launch_rows(const UQKSpatial *d, const void *x, void *y, uint32_t batches, int cols, int emode)
+{
+    if (!g_cus) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n < 1)
+            return uqk_fail(hipErrorInvalidDevice);
+        g_cus = n;
+    }
+    RowsArgs a;
+    a.x = (const int8_t *)x;
+    a.y = (int8_t *)y;
+    a.w = (const int8_t *)d->w;
+    a.epi = (const int4 *)d->epi;
+    a.lut = (const uint8_t *)d->lut;
+    a.ih = d->ih; a.iw = d->iw; a.ow = d->ow; a.ohw = d->oh * d->ow; a.kh = d->kh; a.kw = d->kw;
+    a.pt = d->pt; a.pl = d->pl; a.oc = d->oc; a.oc_pad = d->oc_pad; a.kpad = d->kpad;
+    a.xz = d->xz; a.yz = d->yz; a.lo = d->lo; a.hi = d->hi;
+    a.cols = cols;
+    a.tiles_per_image = (a.ohw + RG_BP - 1) / RG_BP;
+    const uint64_t tiles = (uint64_t)batches * a.tiles_per_image;
+    if (!tiles || tiles > 0x7fffffffULL) return (int)hipErrorInvalidValue;
+    a.tiles = (int)tiles;
+    const unsigned grid = (unsigned)(tiles < (uint64_t)g_cus ? tiles : (uint64_t)g_cus);
+    hipStream_t st;
+    hipEvent_t e0, e1;
+    uqk_next_launch(&st, &e0, &e1);
+    switch (emode) {
+    case 0: hipExtLaunchKernelGGL(k_gemm_rows<0>, dim3(grid), dim3(64 * RG_NW), 0, st, e0, e1, 0u, a); break;
+    case 1: hipExtLaunchKernelGGL(k_gemm_rows<1>, dim3(grid), dim3(64 * RG_NW), 0, st, e0, e1, 0u, a); break;
+    case 2: hipExtLaunchKernelGGL(k_gemm_rows<2>, dim3(grid), dim3(64 * RG_NW), 0, st, e0, e1, 0u, a); break;
+    default: hipExtLaunchKernelGGL(k_gemm_rows<3>, dim3(grid), dim3(64 * RG_NW), 0, st, e0, e1, 0u, a); break;
+    }
+    const int rc = uqk_fail(hipGetLastError());
+    if (!rc) g_launches++;
+    return rc;
+}
 
 extern "C" int uqk_gemm_ok(const UQKSpatial *d)
 {
@@ -401,8 +689,12 @@ extern "C" int uqk_gemm_ok(const UQKSpatial *d)
 static int gemm_tile(const UQKSpatial *d, uint64_t pixels)
 {
     (void)pixels;
+    int cols;
     const bool deep_ok = d->mode == UQK_PW || d->ic % 128 == 0;
-    int tile = d->gemm_tile >= 0 ? d->gemm_tile : d->oc > 128 ? 1 : deep_ok ? 2 : 0;
+    if (d->gemm_tile == 4 || (d->gemm_tile < 0 && rows_fit(d, &cols))) {
+        if (rows_fit(d, &cols)) return 4;
+    }
+    int tile = d->gemm_tile >= 0 && d->gemm_tile < 4 ? d->gemm_tile : d->oc > 128 ? 1 : deep_ok ? 2 : 0;
     if (g_tile_ks[tile] == 128 && !deep_ok) tile -= 2;
     return tile;
 }
@@ -429,8 +721,14 @@ extern "C" int uqk_gemm(const UQKSpatial *d, const void *x, void *y, uint32_t ba
     a.ih = d->ih; a.iw = d->iw; a.ic = d->ic; a.ow = d->ow; a.ohw = d->oh * d->ow;
     a.kw = d->kw; a.sh = d->sh; a.sw = d->sw; a.dh = d->dh; a.dw = d->dw; a.pt = d->pt; a.pl = d->pl;
     a.xz = d->xz; a.yz = d->yz; a.lo = d->lo; a.hi = d->hi;
+    a.rotate = 1;
     const int emode = (d->hi_shift ? 1 : 0) | (d->corr ? 2 : 0);
     const int tile = gemm_tile(d, pixels);
+    if (tile == 4) {
+        int cols = 0;
+        rows_fit(d, &cols);
+        return launch_rows(d, x, y, batches, cols, emode);
+    }
     const int bp = 256, bc = g_tile_bc[tile];
     a.ctiles = (d->oc + bc - 1) / bc;
     const uint64_t blocks = (pixels + bp - 1) / bp * (uint64_t)a.ctiles;

@@ -673,11 +673,11 @@ static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
     const int oc = q[17];
     const int32_t *bias = q + UQ_HEAD, *mult = bias + oc, *shift = mult + oc;
     d->dwwin = o->code == 15 && uqk_dw_win_lds(d) > 0;
-    /* Large-tile GEMM policy (UQ_GEMM=0/1 and UQ_GEMM_TILE=0..3 at load
+    /* Large-tile GEMM policy (UQ_GEMM=0/1 and UQ_GEMM_TILE=0..4 at load
      * time override the automatic choice). */
     const char *ge = getenv("UQ_GEMM"), *gt = getenv("UQ_GEMM_TILE");
     d->gemm = ge && (!strcmp(ge, "0") || !strcmp(ge, "1")) ? atoi(ge) : -1;
-    d->gemm_tile = gt && gt[0] >= '0' && gt[0] <= '3' && !gt[1] ? gt[0] - '0' : -1;
+    d->gemm_tile = gt && gt[0] >= '0' && gt[0] <= '4' && !gt[1] ? gt[0] - '0' : -1;
     d->hi_shift = o->code == 14 || d->dwwin;
     for (int c = 0; c < oc; c++)
         if (shift[c] > -1 || shift[c] < -22) d->hi_shift = 0;

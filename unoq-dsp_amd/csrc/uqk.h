@@ -30,7 +30,7 @@ typedef struct {
     int32_t hi_shift;          /* every shift in [-22, -1]: records fold bias and zero point into c1 */
     int32_t dwwin;             /* depthwise on tap windows (k_dw_win); wdot holds [ky][wk][C] tap words */
     int32_t gemm;              /* large-tile GEMM: -1 when the launch is large enough, 0 never, 1 whenever the shape fits */
-    int32_t gemm_tile;         /* its tile configuration: -1 automatic, else 0..3 (gemm.hip) */
+    int32_t gemm_tile;         /* its tile configuration: -1 automatic, else 0..4 (gemm.hip) */
     const void *w;
     const void *wdot;
     const void *epi;
