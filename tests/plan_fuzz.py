@@ -418,3 +418,34 @@ def gemm_rows_plan(seed):
         except ValueError:
             continue
     raise AssertionError("unreachable")
+
+
+def dw_band_plan(seed):
+    """A depthwise layer for the band kernel: 3x3 or 5x5, stride 1 or 2, 16 to
+    240 channels (channel slices of 1, 2, 3, 5, 6 or 15 groups of 16), maps
+    from 3x3 to 112x112 (one band or many), SAME or explicit padding,
+    optional post table, all requantisation ranges."""
+    rng = Rng(seed, 737373)
+    p = Plan(seed)
+    c = _pick(rng, [16, 32, 48, 64, 80, 96, 240])
+    hw = _pick(rng, [3, 5, 7, 14, 17, 28, 56, 112] if c <= 64 else [3, 7, 14, 28, 56])
+    x = p.input((1, hw, hw, c), zp=int(rng.integers(1, -128, 127)[0]))
+    k = _pick(rng, [3, 5])
+    stride = _pick(rng, [1, 2])
+    if _pick(rng, [0, 1]):
+        padding = "same"
+    else:
+        pt, pb = _geometry(rng, hw, k, stride, 1)
+        padding = (pt, pt, pb, pb)
+    lut = _random_lut(p, rng) if _pick(rng, [0, 0, 1]) else None
+    lo = int(rng.integers(1, -24, -1)[0])
+    for shift in ((lo, 3), (-12, -4), (-20, -1)):
+        try:
+            y = p.depthwise(x, k=k, stride=stride, padding=padding, act=_pick(rng, ["none", "relu", "relu6"]),
+                            q6=int(rng.integers(1, 1, 200)[0]), lut=lut, shift=shift,
+                            zero_mult=_pick(rng, [0.0, 0.3]), w_sigma=_pick(rng, [3, 40, 90]),
+                            bias_sigma=_pick(rng, [0, 2048, 60000]))
+            return p.build(y)
+        except ValueError:
+            continue
+    raise AssertionError("unreachable")

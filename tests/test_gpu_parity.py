@@ -12,8 +12,8 @@ import pytest
 
 import uq_plan as P
 import uq_workloads as W
-from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, dw_mfma_plan, gemm_plan,
-                       gemm_rows_plan, random_plan, pointwise_wide_plan, rows_conv_plan, stem_plan)
+from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, dw_band_plan, dw_mfma_plan,
+                       gemm_plan, gemm_rows_plan, random_plan, pointwise_wide_plan, rows_conv_plan, stem_plan)
 from test_oracle_vs_reference import (BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, softmax_table_plan,
                                       transpose_plan)
 from refs import oracle_run
@@ -439,6 +439,19 @@ def test_kernel_shape_fuzz(lib, maker, seed):
     images = 2
     x = P.random_input(plan, images, seed)
     _assert_same(Graph(plan, lib).run_batch(x, images), _oracle(plan, x, images), f"{maker.__name__} {seed}")
+
+
+@pytest.mark.parametrize("kernel", ["band", "mfma", "win"])
+@pytest.mark.parametrize("seed", range(24))
+def test_depthwise_kernels(lib, kernel, seed, monkeypatch):
+    """Each depthwise kernel forced at load (band, matrix-core window, dot4
+    window), on wide-channel band-shaped plans and matrix-core-shaped ones,
+    one to three images, byte for byte against the oracle."""
+    monkeypatch.setenv("UQ_DW", kernel)
+    plan = dw_band_plan(seed) if seed % 2 == 0 else dw_mfma_plan(100 + seed)
+    images = 1 + seed % 3
+    x = P.random_input(plan, images, seed)
+    _assert_same(Graph(plan, lib).run_batch(x, images), _oracle(plan, x, images), f"depthwise {kernel} {seed}")
 
 
 def test_profile_counts_one_run_per_profiled_batch(lib):

@@ -67,47 +67,6 @@ __device__ __forceinline__ int swz(int row, int c)
     return KS == 64 ? c ^ ((row >> 2) & 3) : c ^ ((row >> 1) & 7);
 }
 
-// Sixteen bytes of value v at offset 16 * v: the source of staged chunks that
-// hold the input zero point (im2col padding), pixel chunks past K (whose
-// weights are zero, so any finite bytes do) and weight chunks past kpad (row
-// 0: zeros), so that every lane of a staging instruction loads from a valid
-// address.
-struct PadRows {
-    uint8_t b[256 * 16];
-};
-static constexpr PadRows make_pad_rows()
-{
-    PadRows p{};
-    for (int i = 0; i < 256 * 16; i++) p.b[i] = (uint8_t)(i >> 4);
-    return p;
-}
-__device__ const PadRows g_pad_rows = make_pad_rows();
-
-// Sixteen bytes from global memory straight into LDS: lane l's bytes land
-// at LDS address lds + 16 * l (lds wave-uniform). Issued through asm (with
-// no memory clobber) so that the compiler, which would otherwise wait for
-// every outstanding LDS load before each LDS read and barrier, leaves the
-// ring's waits to wait_vm. Order against the LDS reads of the same buffer
-// comes from the barriers: a buffer is refilled only after the barrier that
-// follows its last read, and read only after the wait and barrier that
-// follow its fill. M0 is the LDS base of the instruction (one wait state
-// between writing M0 and the load that reads it).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_load16(const void *src, uint32_t lds)
-{
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds) : "m0");
-}
-#pragma clang diagnostic pop
-
-// Wait until at most N of this wave's vector-memory loads are outstanding.
-template <int N>
-__device__ __forceinline__ void wait_vm()
-{
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
-
 // Requantisation records of a block's channels in LDS, one array per field.
 struct EpiLds {
     int *m, *t, *b, *ls;

@@ -678,6 +678,11 @@ static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
     const char *ge = getenv("UQ_GEMM"), *gt = getenv("UQ_GEMM_TILE");
     d->gemm = ge && (!strcmp(ge, "0") || !strcmp(ge, "1")) ? atoi(ge) : -1;
     d->gemm_tile = gt && gt[0] >= '0' && gt[0] <= '4' && !gt[1] ? gt[0] - '0' : -1;
+    /* Depthwise kernel (UQ_DW=band, mfma or win at load time overrides the
+     * automatic choice). */
+    const char *dk = getenv("UQ_DW");
+    d->dwk = !dk ? -1 : !strcmp(dk, "band") ? 0 : !strcmp(dk, "mfma") ? 1 : !strcmp(dk, "win") ? 2 : -1;
+    if (o->code == 15) uqk_dw_band_prepare(d);
     d->hi_shift = o->code == 14 || d->dwwin;
     for (int c = 0; c < oc; c++)
         if (shift[c] > -1 || shift[c] < -22) d->hi_shift = 0;

@@ -120,19 +120,6 @@ struct ConvArgs {
     int add_m, add_s, add_yz, add_lo, add_hi, add_conv_a;
 };
 
-// x / d without a division: ceil(2^32 / d) as a multiply-high, exact when
-// x * d < 2^32 (the rounding error of the magic is below d); d == 1 passes
-// x through. The magic comes from udiv_magic on the host.
-__device__ __forceinline__ unsigned udiv(unsigned x, unsigned d, unsigned magic)
-{
-    return d == 1 ? x : __umulhi(x, magic);
-}
-
-static inline unsigned udiv_magic(unsigned d)
-{
-    return d <= 1 ? 0u : (unsigned)((0x100000000ULL + d - 1) / d);
-}
-
 template <int MODE>
 __device__ __forceinline__ v4i gather16(const ConvArgs &a, const int8_t *base, int iy0, int ix0, bool valid, int kg, int xzw)
 {
@@ -181,16 +168,6 @@ __device__ __forceinline__ v4i gather16(const ConvArgs &a, const int8_t *base, i
     }
 }
 
-// 4x4 byte transpose across a quad of lanes: lane j of the quad ends with
-// byte j of each of the four lanes' words.
-__device__ __forceinline__ int quad_transpose_bytes(int w, int lane)
-{
-    const int j = lane & 3;
-    const int x = __builtin_amdgcn_mov_dpp(w, 0x4E, 0xF, 0xF, true);        // quad_perm [2,3,0,1]
-    const int u = (int)__builtin_amdgcn_perm((unsigned)x, (unsigned)w, j < 2 ? 0x05040100u : 0x03020706u);
-    const int y = __builtin_amdgcn_mov_dpp(u, 0xB1, 0xF, 0xF, true);        // quad_perm [1,0,3,2]
-    return (int)__builtin_amdgcn_perm((unsigned)y, (unsigned)u, (j & 1) ? 0x03070105u : 0x06020400u);
-}
 
 // Stage the block's per-channel records (columns n0 .. n0 + NT*16 - 1; the
 // channels past OC reuse record 0) and the layer's 256-byte post table in
@@ -2268,8 +2245,14 @@ extern "C" int uqk_depthwise(const UQKSpatial *d, const void *x, void *y, uint32
 {
     if (!batches) return 0;
     if (d->dwwin) {
+        // The band kernel by default for 3x3 stride 2 only (29.7 -> 19.8 us
+        // at 64 x 112x112x64): the matrix-core window kernel measured faster
+        // for 5x5 (12.8 / 14.2 against 15.2 / 17.7 us) and level for 3x3
+        // stride 1.
+        if (d->dwb[0] > 0 && (d->dwk == 0 || (d->dwk < 0 && d->kh == 3 && d->sh == 2)))
+            return uqk_dw_band(d, x, y, batches);
         DwMArgs t;
-        if (dw_mfma_plan(d, &t)) return launch_dw_mfma(d, x, y, batches) < 0 ? (int)hipErrorInvalidValue : 0;
+        if (d->dwk != 2 && dw_mfma_plan(d, &t)) return launch_dw_mfma(d, x, y, batches) < 0 ? (int)hipErrorInvalidValue : 0;
         return launch_dw_win(d, x, y, batches) < 0 ? (int)hipErrorInvalidValue : 0;
     }
     const int rc = launch_dw_tile(d, x, y, batches);

@@ -31,6 +31,9 @@ typedef struct {
     int32_t dwwin;             /* depthwise on tap windows (k_dw_win); wdot holds [ky][wk][C] tap words */
     int32_t gemm;              /* large-tile GEMM: -1 when the launch is large enough, 0 never, 1 whenever the shape fits */
     int32_t gemm_tile;         /* its tile configuration: -1 automatic, else 0..4 (gemm.hip) */
+    int32_t dwk;               /* depthwise kernel: -1 automatic, 0 band (dw.hip), 1 matrix-core window, 2 dot4 window */
+    int32_t dwb[4];            /* band depthwise plan (uqk_dw_band_prepare): channel groups per block (0: the layer
+                                * does not fit), output rows per block, chunk swizzle shift and mask */
     const void *w;
     const void *wdot;
     const void *epi;
@@ -49,6 +52,12 @@ enum { UQK_PW = 0, UQK_G16 = 1, UQK_G4 = 2, UQK_G1 = 3, UQK_ROWS16 = 4, UQK_ROWS
  * the layer's shape is outside it (needs C % 4 == 0, square 3x3 or 5x5,
  * stride 1 or 2, no dilation). */
 size_t uqk_dw_win_lds(const UQKSpatial *d);
+
+/* Band depthwise (dw.hip): 3x3/5x5, stride 1/2, C % 16 == 0. prepare fills
+ * d->dwb once when the plan is loaded (reads the geometry fields); the launch
+ * uses that plan (hipErrorInvalidValue if d->dwb[0] is 0). */
+void uqk_dw_band_prepare(UQKSpatial *d);
+int uqk_dw_band(const UQKSpatial *d, const void *x, void *y, uint32_t batches);
 
 /* Fused inverted bottleneck (1x1 expand -> stride-1 depthwise -> 1x1
  * project [-> residual add with the block input]), one workgroup per image.
