@@ -8,11 +8,17 @@ of the batch through every op of the plan (ug_enqueue_device).
 Prints ONE JSON line. Besides the headline images/s it reports:
   roofline      the op with the largest average launch time, its algorithmic
                 bytes (or ops) per launch over its HIP-event duration
+  network_roofline  the step's algorithmic bytes at 8 TB/s against the step
   cpu_baseline  the reference's portable C runtime (oracle/_ref, built from
-                the reference sources) on this host's cores, batch-1 plans
+                the reference sources) on this host's cores, batch-1 plans;
+                cpu_baseline_other: the same for the secondary workloads
   secondary     YOLO26n-shaped detector images/s (320x320, batch 64), int8
-                conv TOPS (1x1 head GEMM, 3x3 implicit GEMM, batch 512) and
-                depthwise HBM GB/s (four cases, batch 64)
+                conv TOPS (1x1 head GEMM, 3x3 implicit GEMM, batch 512),
+                batch-1 1x1 conv latency, host-buffer throughput and latency,
+                depthwise HBM GB/s (four cases, batch 64); each with `frac`
+                against its bound (5.0 POP/s dense int8, or 8 TB/s)
+With --library-gemm it only prints the vendor library's int8 GEMM timings on
+the same GEMM shapes.
 """
 import argparse
 import ctypes as C
@@ -94,18 +100,41 @@ def _cpu_worker(args):
     return done, time.perf_counter() - t0
 
 
-def cpu_baseline(plan, seconds_per_worker=1.5):
+# CPU legs of the other workloads: batch-1 plans of the same layers (the
+# reference runs one image per ug_run call; its plans hold a bounded tensor
+# size, runtime/graph.h:7,9), timed the same way as the headline leg.
+CPU_LEGS = ("dw3s1", "dw3s2", "dw5s1", "dw5s2", "yolo", "head", "conv3x3")
+
+
+def cpu_legs(workload, seconds_per_worker=1.5, legs=CPU_LEGS):
+    """Images/s of the reference's release build on this host's cores for
+    `workload` (the cpu_baseline of the JSON line) and for each of `legs`:
+    one batch-1 plan per worker process, at most 16 processes, all legs in
+    one pool."""
     if not REF_RELEASE.exists():
-        return None
+        return None, {}
     workers = max(1, min(16, len(os.sched_getaffinity(0))))
+    names = [workload] + [n for n in legs if n != workload]
+    plans = {n: W.WORKLOADS[n](images=1)[0] for n in names}
     ctx = mp.get_context("spawn")
     with ctx.Pool(workers) as pool:
-        res = pool.map(_cpu_worker, [(plan, seconds_per_worker, 100 + i) for i in range(workers)])
-    rate = sum(d / t for d, t in res)
-    images = sum(d for d, _ in res)
-    return {"value": round(rate, 2), "unit": "images/s", "cores": workers, "kind": "reference",
-            "sample": f"{images} MobileNetV4-S batch-1 images via ug_run, {workers} processes x ~{seconds_per_worker}s "
-                      f"(reference runtime/graph.c+qnn.c+gemm.c, release macros, gcc -O3)"}
+        res = {n: pool.map(_cpu_worker, [(plans[n], seconds_per_worker, 100 + i) for i in range(workers)])
+               for n in names}
+    out = {}
+    for n in names:
+        rate = sum(d / t for d, t in res[n])
+        costs = P.op_costs(plans[n], 1)
+        entry = {"value": round(rate, 2), "unit": "images/s", "cores": workers, "kind": "reference",
+                 "sample": f"{sum(d for d, _ in res[n])} {n} batch-1 images via ug_run, {workers} processes x "
+                           f"~{seconds_per_worker}s (reference runtime/graph.c+qnn.c+gemm.c, release macros, gcc -O3)"}
+        ops, nbytes = sum(c["ops"] for c in costs), sum(c["bytes"] for c in costs)
+        if n.startswith("dw"):
+            entry["gbps"] = round(rate * nbytes / 1e9, 3)
+        elif n in ("head", "conv3x3"):
+            entry["tops"] = round(rate * ops / 1e12, 4)
+        out[n] = entry
+    head = out.pop(workload)
+    return head, out
 
 
 def roofline_entry(costs, per_op_ns):
@@ -174,30 +203,104 @@ def host_transfer(lib, steps):
     return res
 
 
+def pointwise_latency(lib, steps):
+    """The batch-1 1x1 conv (56x56x32 -> 64): microseconds per call through
+    ug_run_device (device buffers, returns when the output is complete) and
+    through a mailbox session (host buffers, copies included), and the
+    kernel's own time from its HIP events."""
+    plan, images = W.WORKLOADS["pointwise"]()
+    g = Graph(plan, lib)
+    x = P.random_input(plan, images, 3)
+    din = DeviceBuffer(lib, x.nbytes)
+    dout = DeviceBuffer(lib, images * g.output_bytes)
+    din.upload(x)
+    n = max(steps * 10, 50)
+    for _ in range(20):
+        assert lib.ug_run_device(din.ptr, dout.ptr, images) == 0
+    t0 = time.perf_counter()
+    for _ in range(n):
+        assert lib.ug_run_device(din.ptr, dout.ptr, images) == 0
+    run_us = (time.perf_counter() - t0) / n * 1e6
+    g.profile(1)
+    for _ in range(n):
+        assert lib.ug_run_device(din.ptr, dout.ptr, images) == 0
+    counters = g.profile(2)
+    g.profile(0)
+    kernel_us = float(counters[2:2 + lib.ug_op_count()].sum()) / max(int(counters[0]), 1) / 1e3
+    din.free()
+    dout.free()
+    from uq_native import Session
+    with Session(plan, "mailbox", lib) as s:
+        for _ in range(20):
+            s.run(x)
+        t0 = time.perf_counter()
+        for _ in range(n):
+            s.run(x)
+        mailbox_us = (time.perf_counter() - t0) / n * 1e6
+    nbytes = sum(c["bytes"] for c in P.op_costs(plan, images))
+    return {"images": images, "run_device_us": round(run_us, 2), "mailbox_us": round(mailbox_us, 2),
+            "kernel_us": round(kernel_us, 2), "bytes": nbytes,
+            "frac": round(nbytes / (kernel_us * 1e-6) / HBM_PEAK, 4), "bound": "hbm"}
+
+
 def secondary(lib, steps):
     out = {}
     plan, images = W.WORKLOADS["yolo"]()
     g = Graph(plan, lib)
     sec, per_op = time_device(lib, g, images, steps, 2)
+    costs = P.op_costs(plan, images)
+    nbytes = sum(c["bytes"] for c in costs)
     out["yolo"] = {"images": images, "ms": round(sec / steps * 1e3, 4), "images_per_s": round(images * steps / sec, 1),
-                   "gops": round(sum(c["ops"] for c in P.op_costs(plan, images)) / 1e9, 2)}
+                   "gops": round(sum(c["ops"] for c in costs) / 1e9, 2),
+                   "frac": round(nbytes / (sec / steps) / HBM_PEAK, 4), "bound": "hbm (network bytes)"}
     for name in ("head", "conv3x3"):
         plan, images = W.WORKLOADS[name]()
         g = Graph(plan, lib)
         sec, per_op = time_device(lib, g, images, steps, 2)
         ops = sum(c["ops"] for c in P.op_costs(plan, images))
+        kernel_tops = ops / (per_op.sum() * 1e-9) / 1e12
         out[name] = {"images": images, "ms": round(sec / steps * 1e3, 4), "tops": round(ops / (sec / steps) / 1e12, 2),
-                     "kernel_tops": round(ops / (per_op.sum() * 1e-9) / 1e12, 2)}
+                     "kernel_tops": round(kernel_tops, 2), "frac": round(kernel_tops * 1e12 / INT8_PEAK, 4),
+                     "bound": "mfma"}
+    out["pointwise_b1"] = pointwise_latency(lib, steps)
     out["host_transfer"] = host_transfer(lib, max(steps // 2, 3))
     for name in ("dw3s1", "dw3s2", "dw5s1", "dw5s2"):
         plan, images = W.WORKLOADS[name]()
         g = Graph(plan, lib)
         sec, per_op = time_device(lib, g, images, steps, 2)
         nbytes = sum(c["bytes"] for c in P.op_costs(plan, images))
+        kernel_gbps = nbytes / (per_op.sum() * 1e-9) / 1e9
         out[name] = {"images": images, "ms": round(sec / steps * 1e3, 4),
                      "gbps": round(nbytes / (sec / steps) / 1e9, 1),
-                     "kernel_gbps": round(nbytes / (per_op.sum() * 1e-9) / 1e9, 1)}
+                     "kernel_gbps": round(kernel_gbps, 1), "frac": round(kernel_gbps * 1e9 / HBM_PEAK, 4),
+                     "bound": "hbm"}
     return out
+
+
+def library_gemm(reps=20):
+    """The vendor library's int8 GEMM (torch._int_mm: int8 x int8 -> int32,
+    no requantisation) on the head and 3x3 layers' GEMM shapes and on a
+    large square one, random operands, for comparison with the large-tile
+    kernels here."""
+    import torch
+    torch.manual_seed(0)
+    res = {}
+    for name, (m, k, n) in {"head": (25088, 960, 1280), "conv3x3_as_gemm": (3276800, 1152, 128),
+                            "square_8192": (8192, 8192, 8192)}.items():
+        a = torch.randint(-128, 128, (m, k), dtype=torch.int8, device="cuda")
+        b = torch.randint(-128, 128, (n, k), dtype=torch.int8, device="cuda").t()
+        for _ in range(5):
+            torch._int_mm(a, b)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            torch._int_mm(a, b)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        res[name] = {"m": m, "k": k, "n": n, "us": round(us, 1), "tops": round(2 * m * k * n / us / 1e6, 1)}
+        del a, b
+    return res
 
 
 def main():
@@ -211,15 +314,23 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--per-op", action="store_true", help="print the per-op table to stderr")
+    ap.add_argument("--images", type=int, default=0, help="batch size (default: the workload's own)")
+    ap.add_argument("--library-gemm", action="store_true",
+                    help="only time the vendor library's int8 GEMM on the same shapes and print it as JSON")
     args = ap.parse_args()
+    if args.library_gemm:
+        print(json.dumps(library_gemm()), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); images are independent, so N GPUs "
               f"would each run this same per-GPU batch", file=sys.stderr)
         sys.exit(2)
     plan, images = W.WORKLOADS[args.workload]()
+    images = args.images or images
     # The CPU baseline runs first, in child processes, before this process
     # touches the GPU.
-    cpu = None if args.no_cpu else cpu_baseline(W.WORKLOADS[args.workload](images=1)[0])
+    cpu, cpu_other = (None, {}) if args.no_cpu else cpu_legs(args.workload,
+                                                              legs=() if args.no_secondary else CPU_LEGS)
     lib = open_library()
     graph = Graph(plan, lib)
     seconds, per_op_ns = time_device(lib, graph, images, args.steps, args.warmup)
@@ -248,11 +359,16 @@ def main():
                    "parallelism": "single GPU, batch-outer"},
         "roofline": roof,
         "sum_kernel_us": round(float(per_op_ns.sum()) / 1e3, 2),
+        # The whole step against HBM: every op's algorithmic bytes at 8 TB/s.
+        "network_roofline": {"floor_us": round(sum(c["bytes"] for c in costs) / HBM_PEAK * 1e6, 1),
+                             "frac": round(sum(c["bytes"] for c in costs) / HBM_PEAK / (seconds / args.steps), 4)},
     }
     if not args.no_secondary:
         result["secondary"] = secondary(lib, 10)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu
+        if cpu_other:
+            result["cpu_baseline_other"] = cpu_other
     print(json.dumps(result), flush=True)
 
 

@@ -351,6 +351,28 @@ def test_split_batch_matches_single_stream(lib, monkeypatch, name, images):
         _assert_same(outs["2"][i * ob:(i + 1) * ob], _oracle(plan, x[i * ib:(i + 1) * ib], 1), f"{name} image {i}")
 
 
+@pytest.mark.parametrize("kind", ["random", "attention", "constant"])
+@pytest.mark.parametrize("seed", range(12))
+def test_split_batch_fuzz_plans(lib, monkeypatch, kind, seed):
+    """Random, attention and constant-operand plans at 130 images: two image
+    slices (65 + 65, on two streams) give the single-stream bytes, and the
+    images on both sides of the slice boundary and at the batch ends match
+    the oracle."""
+    ops = {"random": None, "attention": ATTENTION_OPS, "constant": CONSTANT_OPS}[kind]
+    plan = random_plan({"random": 1400, "attention": 7400, "constant": 8400}[kind] + seed, ops=ops)
+    images = 130
+    x = P.random_input(plan, images, seed)
+    outs = {}
+    for streams in ("1", "2"):
+        monkeypatch.setenv("UQ_STREAMS", streams)
+        outs[streams] = Graph(plan, lib).run_batch(x, images)
+    _assert_same(outs["2"], outs["1"], f"{kind} plan {seed}: two slices vs one stream")
+    ib, ob = P.input_bytes(plan), P.output_bytes(plan)
+    for i in (0, 64, 65, 129):
+        _assert_same(outs["2"][i * ob:(i + 1) * ob], _oracle(plan, x[i * ib:(i + 1) * ib], 1),
+                     f"{kind} plan {seed} image {i}")
+
+
 def test_split_batches_continue_across_calls(lib, monkeypatch):
     """Consecutive identical device batches keep their two slices on their
     own streams without joining; a batch on other buffers, a snapshot taken
