@@ -449,3 +449,50 @@ def dw_band_plan(seed):
         except ValueError:
             continue
     raise AssertionError("unreachable")
+
+
+def ib_plan(seed):
+    """An inverted bottleneck of the shape the fused kernel takes (behind a
+    post table, so that the block input is the library's own buffer): 1x1
+    expand from 32 to 256 channels to up to 512, a 3x3 or 5x5 stride-1 SAME
+    depthwise, 1x1 project, and a residual add with the block input (either
+    operand order) when the channel counts match; maps from 1x1 to 28x28
+    within the workgroup's LDS, post tables, activations and all
+    requantisation ranges."""
+    rng = Rng(seed, 515151)
+    p = Plan(seed)
+    while True:
+        hw = int(_pick(rng, [1, 2, 3, 5, 7, 9, 14, 16, 20, 28]))
+        cin = int(_pick(rng, [32, 64, 96, 128, 256]))
+        ce = int(_pick(rng, [64, 96, 128, 192, 256, 384, 512]))
+        ks = int(_pick(rng, [3, 5]))
+        add = bool(_pick(rng, [0, 1, 1]))
+        cout = cin if add else int(_pick(rng, [32, 64, 96, 128]))
+        P = hw * hw
+        lds = (P * (cin + 16) + ce * (hw + ks - 1) ** 2 + P * (ce + 16) + 64 * ce + 32 * cout + 2048 + 768 + 4 * P
+               + 4 * ks * (2 if ks > 4 else 1) * ce)
+        if lds <= 163840 and P * cout <= ce * (hw + ks - 1) ** 2:
+            break
+    x = p.input((1, hw, hw, cin), zp=int(rng.integers(1, -128, 127)[0]))
+    x = p.lut(x, _random_lut(p, rng))
+
+    def layer(make):
+        lo = int(rng.integers(1, -24, -1)[0])
+        for shift in ((lo, 3), (-12, -4), (-20, -1)):
+            try:
+                return make(shift)
+            except ValueError:
+                continue
+        raise AssertionError("unreachable")
+
+    def opts():
+        return dict(act=_pick(rng, ["none", "relu", "relu6"]), q6=int(rng.integers(1, 1, 200)[0]),
+                    lut=_random_lut(p, rng) if _pick(rng, [0, 0, 1]) else None, w_sigma=_pick(rng, [3, 40, 90]))
+    e = layer(lambda shift: p.conv(x, ce, k=1, shift=shift, **opts()))
+    d = layer(lambda shift: p.depthwise(e, k=ks, stride=1, padding="same", shift=shift,
+                                         bias_sigma=_pick(rng, [0, 2048, 60000]), **opts()))
+    z = layer(lambda shift: p.conv(d, cout, k=1, shift=shift, **opts()))
+    if add:
+        z = p.add(x, z, act=_pick(rng, ["none", "relu", "relu6"])) if _pick(rng, [0, 1]) else \
+            p.add(z, x, act=_pick(rng, ["none", "relu", "relu6"]))
+    return p.build(z)

@@ -13,7 +13,7 @@ import pytest
 import uq_plan as P
 import uq_workloads as W
 from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, dw_band_plan, dw_mfma_plan,
-                       gemm_plan, gemm_rows_plan, random_plan, pointwise_wide_plan, rows_conv_plan, stem_plan)
+                       gemm_plan, gemm_rows_plan, ib_plan, random_plan, pointwise_wide_plan, rows_conv_plan, stem_plan)
 from test_oracle_vs_reference import (BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, softmax_table_plan,
                                       transpose_plan)
 from refs import oracle_run
@@ -259,9 +259,10 @@ def test_bad_sizes_rejected(lib):
 
 @pytest.mark.parametrize("name,images", [("mnv4", 3), ("mnv4", 256)])
 def test_fused_bottleneck_opt_in(lib, monkeypatch, name, images):
-    """UQ_FUSE_BOTTLENECK=1 at load time runs 1x1 -> depthwise -> 1x1 (-> add)
-    groups as one launch; the bytes must not change, and snapshots of a group's
-    inner tensors are rebuilt from the group input."""
+    """1x1 -> depthwise -> 1x1 (-> add) groups run as one launch (the default;
+    UQ_FUSE_BOTTLENECK=1 asks for it explicitly); the bytes must not change,
+    and snapshots of a group's inner tensors are rebuilt from the group
+    input."""
     plan, _ = W.WORKLOADS[name]()
     x = P.random_input(plan, images, 41)
     monkeypatch.setenv("UQ_FUSE_BOTTLENECK", "1")
@@ -278,6 +279,27 @@ def test_fused_bottleneck_opt_in(lib, monkeypatch, name, images):
         nbytes = images * recs[t][1]
         _, want = oracle_run(plan, x, images, P.output_bytes(plan), snap=t, snap_bytes=nbytes)
         _assert_same(g.snapshot_images(t, nbytes), want, f"fused snapshot tensor {t}")
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_fused_bottleneck_plans(lib, monkeypatch, seed):
+    """Random inverted bottlenecks run fused: the fused kernel runs, and one
+    to three images match the oracle byte for byte, as they do with fusion
+    off (UQ_FUSE_BOTTLENECK=0)."""
+    monkeypatch.setenv("UQ_FUSE_BOTTLENECK", "1")
+    plan = ib_plan(seed)
+    images = 1 + seed % 3
+    x = P.random_input(plan, images, seed)
+    g = Graph(plan, lib)
+    before = lib.uqk_ib_launches()
+    y = g.run_batch(x, images)
+    assert lib.uqk_ib_launches() > before, "the fused bottleneck kernel did not run"
+    want = _oracle(plan, x, images)
+    _assert_same(y, want, f"fused bottleneck plan {seed}")
+    monkeypatch.setenv("UQ_FUSE_BOTTLENECK", "0")
+    before = lib.uqk_ib_launches()
+    _assert_same(Graph(plan, lib).run_batch(x, images), want, f"unfused bottleneck plan {seed}")
+    assert lib.uqk_ib_launches() == before
 
 
 @pytest.mark.parametrize("seed", range(40))

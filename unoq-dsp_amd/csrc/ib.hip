@@ -1,0 +1,506 @@
+// Fused inverted bottleneck for gfx950: 1x1 expand -> stride-1 depthwise ->
+// 1x1 project [-> residual add with the block input], one workgroup of eight
+// waves per image, every intermediate in LDS (the reference runs the three
+// or four ops one after another through HBM: qnn.c:1074-1246 for the 1x1
+// convs, qnn.c:807-983 for the depthwise, qnn.c:1248-1290 for the add).
+// Each phase is the arithmetic of the separate kernels (same operand bytes,
+// the same epilogue records, requantisation and post tables), so the bytes
+// are identical; only the HBM round trips of the expanded tensors and three
+// of the four launches go.
+//
+// Phases, separated by barriers:
+//   0  the image's input rows, the three layers' records, the add and post
+//      tables into LDS; the depthwise window planes filled with its input
+//      zero point.
+//   1  expand: 32x32 tiles on v_mfma_i32_32x32x32_i8 with the pixels as the
+//      MFMA rows (from LDS) and the weights as its columns (16-byte loads
+//      from HBM/L2), so that a lane's 16 results share one channel and its
+//      requantisation record stays in registers while the wave's tiles share
+//      a channel tile. A 4x4 byte transpose across each lane quad turns four
+//      pixels of one channel into four channels of one pixel: 4-byte LDS
+//      writes into the window plane of the channels' 16-channel group, at
+//      the pixel's padded position.
+//   2  depthwise on the matrix cores as in k_dw_mfma: per 16 pixels x 16
+//      channels, one v_mfma_i32_16x16x64_i8 per four taps, whose A rows are
+//      16-byte reads of the window planes and whose B is block diagonal (a
+//      lane's tap weight at its channel's byte). Output rows of Ce bytes
+//      (padded by 16) in LDS.
+//   3  project: 16x16 tiles on v_mfma_i32_16x16x64_i8 (finer work items for
+//      the small maps) with the depthwise rows as the MFMA rows; the
+//      residual add, if fused, per byte from the input rows still in LDS;
+//      the output staged in LDS (over the window planes, free by then) and
+//      copied out with 16-byte stores.
+//
+// LDS (bytes): X [P][Cin + 16] | E [Ce / 16][rows_p * cols_p][16] (later the
+// output stage [P][Cout]) | D [P][Ce + 16] | records (expand, depthwise,
+// project; 32 bytes per channel) | add tables [2][256] int32 | post tables
+// [3][256] | padded window position of each pixel [P] int32 | depthwise tap
+// words [ks][ks > 4 ? 2 : 1][Ce]. Rows padded by 16 bytes keep 32-row
+// fragment reads off a single bank group.
+#include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
+#include <stdint.h>
+#include "uqk.h"
+#include "uqk_device.h"
+#include "uqk_internal.h"
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int IB_WAVES = 16;
+constexpr int IB_LDS_MAX = 163840;
+
+struct IbArgs {
+    const int8_t *x;
+    int8_t *y;
+    int P, H, W, Cin, Ce, Cout, pt, pl;
+    int rows_p, cols_p;        // depthwise window plane (padded map)
+    int xs, ds;                // LDS row strides of X and D
+    unsigned m_w;              // udiv_magic(W)
+    unsigned m_cq;             // udiv_magic(Cin / 16)
+    const int8_t *we;          // expand weights [>= Ce][kpe]
+    const int4 *epi_e;
+    const uint8_t *lut_e;
+    int kpe, e_mode, e_yz, e_lo, e_hi;
+    const int *dww;            // depthwise tap words [ky][k][Ce]
+    const int4 *epi_d;
+    const uint8_t *lut_d;
+    int d_mode, d_yz, d_lo, d_hi, d_xz;
+    const int8_t *wp;          // project weights [>= Cout][kpp]
+    const int4 *epi_p;
+    const uint8_t *lut_p;
+    int kpp, p_mode, p_yz, p_lo, p_hi;
+    int has_add, add_x_first;
+    const int *add_tab;
+    int a_m, a_s, a_yz, a_lo, a_hi;
+    long long a_c1, a_thr;     // the add's rescale as one multiply-add (s < 0)
+    int a_hs;                  // its high-word shift, -s - 1
+    int ks;                    // depthwise kernel size
+    int o_e, o_d, o_re, o_rd, o_rp, o_at, o_lut, o_po, o_tw;   // LDS offsets
+};
+
+// Fragments of a wave's weight tile: rows ct*32 + (lane & 31), the 16-byte
+// K slice of each 32-byte step chosen by lane >> 5.
+template <int MAXK>
+__device__ __forceinline__ void ib_load_weights(v4i (&wf)[MAXK], const int8_t *w, int kp, int ks, int ct)
+{
+    const int lane = threadIdx.x & 63;
+    const int8_t *wr = w + (long)(ct * 32 + (lane & 31)) * kp + (lane >> 5) * 16;
+#pragma unroll
+    for (int s = 0; s < MAXK; s++)
+        if (s < ks) wf[s] = *(const v4i *)(wr + s * 32);
+}
+
+// This wave's range of (channel tile, pixel tile) items of a 1x1 phase.
+__device__ __forceinline__ void ib_items(int ctiles, int P, int &i0, int &i1)
+{
+    const int wave = threadIdx.x >> 6, items = ctiles * ((P + 31) >> 5);
+    i0 = wave * items / IB_WAVES;
+    i1 = (wave + 1) * items / IB_WAVES;
+}
+
+// A 1x1 GEMM phase over the image's P pixels: pixel tiles of 32 (MFMA rows,
+// rows of `src` in LDS with stride ss, clamped to P - 1 past the image) by
+// channel tiles of 32 (columns: weights `w`, row stride kp, K = 32 * ks
+// bytes). Each wave takes a contiguous range of (channel tile, pixel tile)
+// items (ib_items), channel tile major, and reloads its weight fragments
+// (wf, of channel tile `loaded`) and its channel's record only when the
+// channel tile changes. `sink(p, c, word)` receives, per lane and for each
+// of its four pixel groups, the requantised bytes of channels c .. c + 3 of
+// pixel p (p < P only).
+template <int MAXK, bool HI, bool CORR, bool LUT, typename Sink>
+__device__ __forceinline__ void ib_gemm(const int8_t *smem, v4i (&wf)[MAXK], int &loaded, const int8_t *w, int kp,
+                                        int ks, const int8_t *src, int ss, int P, int ctiles, int rec_off, int yz,
+                                        int lo, int hi, const int8_t *lut, Sink sink)
+{
+    const int lane = threadIdx.x & 63;
+    const int fr = lane & 31, fh = lane >> 5;
+    const int ptiles = (P + 31) >> 5;
+    int i0, i1;
+    ib_items(ctiles, P, i0, i1);
+    const int vlo = vgpr(lo), vhi = vgpr(hi);
+    Epi e = {};
+    // (channel tile, pixel tile) of the item, stepped along without divisions.
+    int ct = i0 / ptiles, pt = i0 - ct * ptiles;
+    for (int item = i0; item < i1; item++, pt = pt + 1 < ptiles ? pt + 1 : 0, ct += pt == 0) {
+        if (ct != loaded) {
+            ib_load_weights<MAXK>(wf, w, kp, ks, ct);
+            loaded = ct;
+        }
+        e = load_epi((const int4 *)(smem + rec_off), ct * 32 + fr);
+        const int8_t *sr = src + __mul24(min(pt * 32 + fr, P - 1), ss) + fh * 16;
+        v16i acc;
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[r] = 0;
+#pragma unroll
+        for (int s = 0; s < MAXK; s++)
+            if (s < ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i *)(sr + s * 32), wf[s], acc, 0, 0, 0);
+        // acc[4g + i]: pixel pt*32 + 8g + 4fh + i, channel ct*32 + fr.
+        const int c = ct * 32 + (fr & ~3);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            int v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[i] = conv_requant<HI, CORR>(acc[4 * g + i], e, yz, vlo, vhi);
+                if (LUT) v[i] = lut[v[i] + 128];
+            }
+            const int word = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
+            const int p = pt * 32 + 8 * g + 4 * fh + (lane & 3);
+            if (p < P) sink(p, c, word);
+        }
+    }
+}
+
+// ib_gemm with the requantisation variant (a wave-uniform mode) and the
+// presence of a post table as template arguments.
+template <int MAXK, typename Sink>
+__device__ __forceinline__ void ib_gemm_mode(int mode, const int8_t *smem, v4i (&wf)[MAXK], int &loaded,
+                                             const int8_t *w, int kp, int ks, const int8_t *src, int ss, int P,
+                                             int ctiles, int rec_off, int yz, int lo, int hi, const int8_t *lut,
+                                             Sink sink)
+{
+#define IB_GEMM(H, C, L) \
+    ib_gemm<MAXK, H, C, L>(smem, wf, loaded, w, kp, ks, src, ss, P, ctiles, rec_off, yz, lo, hi, lut, sink)
+    switch (mode * 2 + (lut != nullptr)) {
+    case 0: IB_GEMM(false, false, false); break;
+    case 1: IB_GEMM(false, false, true); break;
+    case 2: IB_GEMM(true, false, false); break;
+    case 3: IB_GEMM(true, false, true); break;
+    case 4: IB_GEMM(false, true, false); break;
+    case 5: IB_GEMM(false, true, true); break;
+    case 6: IB_GEMM(true, true, false); break;
+    default: IB_GEMM(true, true, true); break;
+    }
+#undef IB_GEMM
+}
+
+// The project phase's GEMM, in 16x16 tiles on v_mfma_i32_16x16x64_i8 (finer
+// items than 32x32 tiles: a 7x7 map has only two 32-pixel tiles): pixel
+// tiles of 16 (rows of `src`, stride ss) by channel tiles of 16 (weights
+// `w`, row stride kp, zero past the K bytes, so that the source bytes a K
+// tail reads past its rows add nothing), K = 64 * ks bytes. Items as in
+// ib_gemm. `sink(p, c, word)`: channels c .. c + 3 of pixel p.
+template <int MAXK, bool HI, bool CORR, bool LUT, typename Sink>
+__device__ __forceinline__ void ib_gemm16(const int8_t *smem, const int8_t *w, int kp, int ks, const int8_t *src,
+                                          int ss, int P, int ctiles, int rec_off, int yz, int lo, int hi,
+                                          const int8_t *lut, Sink sink)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int ptiles = (P + 15) >> 4, items = ctiles * ptiles;
+    const int i0 = wave * items / IB_WAVES, i1 = (wave + 1) * items / IB_WAVES;
+    const int vlo = vgpr(lo), vhi = vgpr(hi);
+    v4i wf[MAXK];
+    Epi e = {};
+    int loaded = -1;
+    int ct = i0 / ptiles, pt = i0 - ct * ptiles;
+    for (int item = i0; item < i1; item++, pt = pt + 1 < ptiles ? pt + 1 : 0, ct += pt == 0) {
+        if (ct != loaded) {
+            const int8_t *wr = w + (long)(ct * 16 + lr) * kp + lg * 16;
+#pragma unroll
+            for (int s = 0; s < MAXK; s++)
+                if (s < ks) wf[s] = *(const v4i *)(wr + s * 64);
+            e = load_epi((const int4 *)(smem + rec_off), ct * 16 + lr);
+            loaded = ct;
+        }
+        const int8_t *sr = src + __mul24(min(pt * 16 + lr, P - 1), ss) + lg * 16;
+        v4i acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < MAXK; s++)
+            if (s < ks) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(const v4i *)(sr + s * 64), wf[s], acc, 0, 0, 0);
+        // acc[i]: pixel pt*16 + 4*lg + i, channel ct*16 + lr.
+        int v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            v[i] = conv_requant<HI, CORR>(acc[i], e, yz, vlo, vhi);
+            if (LUT) v[i] = lut[v[i] + 128];
+        }
+        const int word = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
+        const int p = pt * 16 + lg * 4 + (lane & 3);
+        if (p < P) sink(p, ct * 16 + (lr & ~3), word);
+    }
+}
+
+template <int MAXK, typename Sink>
+__device__ __forceinline__ void ib_gemm16_mode(int mode, const int8_t *smem, const int8_t *w, int kp, int ks,
+                                               const int8_t *src, int ss, int P, int ctiles, int rec_off, int yz,
+                                               int lo, int hi, const int8_t *lut, Sink sink)
+{
+#define IB_GEMM(H, C, L) ib_gemm16<MAXK, H, C, L>(smem, w, kp, ks, src, ss, P, ctiles, rec_off, yz, lo, hi, lut, sink)
+    switch (mode * 2 + (lut != nullptr)) {
+    case 0: IB_GEMM(false, false, false); break;
+    case 1: IB_GEMM(false, false, true); break;
+    case 2: IB_GEMM(true, false, false); break;
+    case 3: IB_GEMM(true, false, true); break;
+    case 4: IB_GEMM(false, true, false); break;
+    case 5: IB_GEMM(false, true, true); break;
+    case 6: IB_GEMM(true, true, false); break;
+    default: IB_GEMM(true, true, true); break;
+    }
+#undef IB_GEMM
+}
+
+// Depthwise phase: items (16-channel group, 16-pixel tile), group major, a
+// contiguous range per wave; the block-diagonal tap operands (from the tap
+// words staged in LDS) and the channel's record are rebuilt when the group
+// changes.
+template <int KS, bool HI, bool CORR, bool LUT>
+__device__ __forceinline__ void ib_dw(const IbArgs &a, const int8_t *smem, const int8_t *E, int8_t *D,
+                                      const int8_t *lut_s, const int *padoff, const int *tw, int plane)
+{
+    constexpr int T = KS * KS, NG = (T + 3) / 4, NWK = KS > 4 ? 2 : 1;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int tiles = (a.P + 15) >> 4, items = (a.Ce >> 4) * tiles;
+    const int i0 = wave * items / IB_WAVES, i1 = (wave + 1) * items / IB_WAVES;
+    const int vlo = vgpr(a.d_lo), vhi = vgpr(a.d_hi);
+    const int corner = a.pt * a.cols_p + a.pl;
+    int off[NG];
+#pragma unroll
+    for (int m = 0; m < NG; m++) {
+        const int t = 4 * m + lg, ky = t / KS, kx = t - ky * KS;
+        off[m] = t < T ? (ky * a.cols_p + kx) * 16 : 0;
+    }
+    v4i B[NG];
+    Epi e = {};
+    int loaded = -1;
+    // (group, tile) of the item, stepped along without divisions; gplane is
+    // the group's window plane less the window corner.
+    int g = i0 / tiles, t16 = i0 - g * tiles;
+    const int8_t *gplane = E;
+    for (int item = i0; item < i1; item++, t16 = t16 + 1 < tiles ? t16 + 1 : 0, g += t16 == 0) {
+        if (g != loaded) {
+            gplane = E + (g * plane - corner) * 16;
+#pragma unroll
+            for (int m = 0; m < NG; m++) {
+                const int t = 4 * m + lg, ky = t / KS, kx = t - ky * KS;
+                int wb = 0;
+                if (t < T) wb = (tw[(ky * NWK + (kx >> 2)) * a.Ce + g * 16 + lr] >> (8 * (kx & 3))) & 0xff;
+                const int word = wb << (8 * (lr & 3)), q = lr >> 2;
+                B[m] = (v4i){q == 0 ? word : 0, q == 1 ? word : 0, q == 2 ? word : 0, q == 3 ? word : 0};
+            }
+            e = load_epi((const int4 *)(smem + a.o_rd), g * 16 + lr);
+            loaded = g;
+        }
+        // The window corner of pixel p is its padded position less (pt, pl).
+        const int p = min(t16 * 16 + lr, a.P - 1);
+        const int8_t *base = gplane + padoff[p] * 16;
+        v4i acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int m = 0; m < NG; m++)
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(const v4i *)(base + off[m]), B[m], acc, 0, 0, 0);
+        // acc[i]: pixel t16*16 + 4*lg + i, channel g*16 + lr.
+        int v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            v[i] = conv_requant<HI, CORR>(acc[i], e, a.d_yz, vlo, vhi);
+            if (LUT) v[i] = lut_s[256 + v[i] + 128];
+        }
+        const int word = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
+        const int px = t16 * 16 + lg * 4 + (lane & 3);
+        if (px < a.P) *(int *)(D + __mul24(px, a.ds) + g * 16 + (lr & ~3)) = word;
+    }
+}
+
+template <int KS>
+__global__ __launch_bounds__(64 * IB_WAVES) void k_ib(IbArgs a)
+{
+    constexpr int NT = 64 * IB_WAVES;
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    int8_t *X = smem, *E = smem + a.o_e, *D = smem + a.o_d;
+    int8_t *lut_s = smem + a.o_lut;
+    const int *at = (const int *)(smem + a.o_at);
+    int *padoff = (int *)(smem + a.o_po);
+    const int tid = threadIdx.x;
+    const long n = blockIdx.x;
+    const int plane = a.rows_p * a.cols_p;
+    const int *tw = (const int *)(smem + a.o_tw);
+
+    // Phase 0.
+    {
+        const int8_t *xin = a.x + n * a.P * a.Cin;
+        const int cq = a.Cin >> 4, chunks = a.P * cq;
+        for (int q = tid; q < chunks; q += NT) {
+            const int p = (int)udiv((unsigned)q, (unsigned)cq, a.m_cq), j = q - p * cq;
+            *(v4i *)(X + p * a.xs + j * 16) = *(const v4i *)(xin + (long)q * 16);
+        }
+        const int xzw = (a.d_xz & 0xff) * 0x01010101;
+        const v4i xzv = {xzw, xzw, xzw, xzw};
+        for (int q = tid; q < (a.Ce >> 4) * plane; q += NT) ((v4i *)E)[q] = xzv;
+        for (int i = tid; i < 2 * a.Ce; i += NT) {
+            ((int4 *)(smem + a.o_re))[i] = a.epi_e[i];
+            ((int4 *)(smem + a.o_rd))[i] = a.epi_d[i];
+        }
+        for (int i = tid; i < 2 * a.Cout; i += NT) ((int4 *)(smem + a.o_rp))[i] = a.epi_p[i];
+        for (int i = tid; i < a.ks * (a.ks > 4 ? 2 : 1) * a.Ce; i += NT) ((int *)(smem + a.o_tw))[i] = a.dww[i];
+        if (a.has_add)
+            for (int i = tid; i < 512; i += NT) ((int *)(smem + a.o_at))[i] = a.add_tab[i];
+        // Padded window position of each pixel.
+        for (int p = tid; p < a.P; p += NT) {
+            const int y = (int)udiv((unsigned)p, (unsigned)a.W, a.m_w), x = p - y * a.W;
+            padoff[p] = (y + a.pt) * a.cols_p + x + a.pl;
+        }
+        if (tid < 64) {
+            if (a.lut_e) ((int *)lut_s)[tid] = ((const int *)a.lut_e)[tid];
+            if (a.lut_d) ((int *)(lut_s + 256))[tid] = ((const int *)a.lut_d)[tid];
+            if (a.lut_p) ((int *)(lut_s + 512))[tid] = ((const int *)a.lut_p)[tid];
+        }
+    }
+    __syncthreads();
+
+    // Phase 1: expand into the window planes.
+    v4i wfe[8];
+    int wfe_ct = -1;
+    ib_gemm_mode<8>(a.e_mode, smem, wfe, wfe_ct, a.we, a.kpe, a.Cin >> 5, X, a.xs, a.P, a.Ce >> 5, a.o_re, a.e_yz,
+                    a.e_lo, a.e_hi, a.lut_e ? lut_s : nullptr, [&](int p, int c, int word) {
+                        *(int *)(E + (__mul24(c >> 4, plane) + padoff[p]) * 16 + (c & 15)) = word;
+                    });
+    __syncthreads();
+
+    // Phase 2: depthwise into D.
+#define IB_DW(H, C, L) ib_dw<KS, H, C, L>(a, smem, E, D, lut_s, padoff, tw, plane)
+    switch (a.d_mode * 2 + (a.lut_d != nullptr)) {
+    case 0: IB_DW(false, false, false); break;
+    case 1: IB_DW(false, false, true); break;
+    case 2: IB_DW(true, false, false); break;
+    case 3: IB_DW(true, false, true); break;
+    case 4: IB_DW(false, true, false); break;
+    case 5: IB_DW(false, true, true); break;
+    case 6: IB_DW(true, true, false); break;
+    default: IB_DW(true, true, true); break;
+    }
+#undef IB_DW
+    __syncthreads();
+
+    // Phase 3: project (+ residual add) into the output stage over E, then
+    // out with 16-byte stores.
+    // The add's rescale (qnn.c:61-83: rounding doubling high multiply, then
+    // a rounding right shift by n = -s) as one multiply-add: for n >= 1,
+    // floor((floor((v*m + 2^30) / 2^31) + 2^(n-1) - [h < 0]) / 2^n) =
+    // floor((v*m + 2^30 + 2^(30+n) - [v*m < -2^30] * 2^31) / 2^(31+n)), whose
+    // high word shifted by n - 1 is the result (a_c1, a_thr, a_hs from the
+    // host); for s >= 0, (((v << s) * m + 2^30) >> 31).
+    int8_t *S = E;
+    const int *atab = at + (a.add_x_first ? 0 : 256), *btab = at + (a.add_x_first ? 256 : 0);
+    auto project_sink = [&](int p, int c, int word) {
+        if (a.has_add) {
+            const int xr = *(const int *)(X + __mul24(p, a.xs) + c);
+            const int vlo = vgpr(a.a_lo), vhi = vgpr(a.a_hi);
+            int z[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int sum = atab[sbyte(xr, i) + 128] + btab[sbyte(word, i) + 128];
+                int r;
+                if (a.a_s < 0) {
+                    long long q = (long long)sum * a.a_m + a.a_c1;
+                    if (q < a.a_thr) q -= 1LL << 31;
+                    r = (int)(q >> 32) >> a.a_hs;
+                } else {
+                    r = (int)(((long long)(int)((unsigned)sum << a.a_s) * a.a_m + (1LL << 30)) >> 31);
+                }
+                z[i] = med3(r + a.a_yz, vlo, vhi);
+            }
+            word = pack4(z[0], z[1], z[2], z[3]);
+        }
+        *(int *)(S + __mul24(p, a.Cout) + c) = word;
+    };
+    // 32x32 tiles when every wave gets one, else 16x16 tiles.
+    if ((a.Cout >> 5) * ((a.P + 31) >> 5) >= IB_WAVES) {
+        v4i wfp[16];
+        int wfp_ct = -1;
+        ib_gemm_mode<16>(a.p_mode, smem, wfp, wfp_ct, a.wp, a.kpp, a.Ce >> 5, D, a.ds, a.P, a.Cout >> 5, a.o_rp,
+                         a.p_yz, a.p_lo, a.p_hi, a.lut_p ? lut_s + 512 : nullptr, project_sink);
+    } else {
+        ib_gemm16_mode<8>(a.p_mode, smem, a.wp, a.kpp, (a.Ce + 63) >> 6, D, a.ds, a.P, a.Cout >> 4, a.o_rp, a.p_yz,
+                          a.p_lo, a.p_hi, a.lut_p ? lut_s + 512 : nullptr, project_sink);
+    }
+    __syncthreads();
+    int8_t *yim = a.y + n * a.P * a.Cout;
+    for (int q = tid; q < (a.P * a.Cout) >> 4; q += NT) ((v4i *)yim)[q] = ((const v4i *)S)[q];
+}
+
+// LDS layout of one workgroup (see the file header); 0 when the block does
+// not fit this kernel: 32-multiple channel counts (K steps and tiles of
+// 32), Cin <= 256, Ce <= 512, a 3x3 or 5x5 depthwise, the output stage
+// within the window planes and the layout within the 160 KiB a workgroup
+// can hold.
+extern "C" size_t uqk_ib_lds(int P, int H, int W, int Cin, int Ce, int Cout, int ks, size_t *offsets)
+{
+    if (P < 1 || P != H * W || Cin % 32 || Ce % 32 || Cout % 32 || Cin > 256 || Ce > 512 || (ks != 3 && ks != 5))
+        return 0;
+    size_t o = 0, off[9];
+    o += (size_t)P * (Cin + 16);                                        // X
+    off[0] = o; o += (size_t)(Ce / 16) * (H + ks - 1) * (W + ks - 1) * 16; // E planes
+    off[1] = o; o += (size_t)P * (Ce + 16);                             // D
+    off[2] = o; o += (size_t)Ce * 32;                                   // expand records
+    off[3] = o; o += (size_t)Ce * 32;                                   // depthwise records
+    off[4] = o; o += (size_t)Cout * 32;                                 // project records
+    off[5] = o; o += 512 * 4;                                           // add tables
+    off[6] = o; o += 3 * 256;                                           // post tables
+    off[7] = o; o += (size_t)P * 4;                                     // padded positions
+    off[8] = o; o += (size_t)ks * (ks > 4 ? 2 : 1) * Ce * 4;            // depthwise tap words
+    if (offsets) for (int i = 0; i < 9; i++) offsets[i] = off[i];
+    // The output stage [P][Cout] lies over the window planes.
+    if ((size_t)P * Cout > off[1] - off[0]) return 0;
+    return o <= (size_t)IB_LDS_MAX ? o : 0;
+}
+
+static uint64_t g_ib_launches;   // successful launches, for tests that must know the fused kernel ran
+
+// Launches of the fused bottleneck kernel since the library was loaded (a
+// test hook; not part of the plan ABI).
+extern "C" uint64_t uqk_ib_launches(void) { return g_ib_launches; }
+
+extern "C" int uqk_ib(const UQKIb *f, const void *x, void *y, uint32_t images)
+{
+    if (!images) return 0;
+    size_t off[9];
+    const size_t lds = uqk_ib_lds(f->P, f->H, f->W, f->Cin, f->Ce, f->Cout, f->ks, off);
+    if (!lds || images > 0x7fffffffu) return (int)hipErrorInvalidValue;
+    IbArgs a;
+    a.x = (const int8_t *)x; a.y = (int8_t *)y;
+    a.P = f->P; a.H = f->H; a.W = f->W; a.Cin = f->Cin; a.Ce = f->Ce; a.Cout = f->Cout; a.pt = f->pt; a.pl = f->pl;
+    a.rows_p = f->H + f->ks - 1; a.cols_p = f->W + f->ks - 1;
+    a.xs = f->Cin + 16; a.ds = f->Ce + 16;
+    a.m_w = udiv_magic((unsigned)f->W); a.m_cq = udiv_magic((unsigned)(f->Cin / 16));
+    a.we = (const int8_t *)f->we; a.epi_e = (const int4 *)f->epi_e; a.lut_e = (const uint8_t *)f->lut_e;
+    a.kpe = f->kpe; a.e_mode = f->e_mode; a.e_yz = f->e_yz; a.e_lo = f->e_lo; a.e_hi = f->e_hi;
+    a.dww = (const int *)f->dww; a.epi_d = (const int4 *)f->epi_d; a.lut_d = (const uint8_t *)f->lut_d;
+    a.d_mode = f->d_mode; a.d_yz = f->d_yz; a.d_lo = f->d_lo; a.d_hi = f->d_hi; a.d_xz = f->d_xz;
+    a.wp = (const int8_t *)f->wp; a.epi_p = (const int4 *)f->epi_p; a.lut_p = (const uint8_t *)f->lut_p;
+    a.kpp = f->kpp; a.p_mode = f->p_mode; a.p_yz = f->p_yz; a.p_lo = f->p_lo; a.p_hi = f->p_hi;
+    a.has_add = f->has_add; a.add_x_first = f->add_x_first; a.add_tab = (const int *)f->add_tab;
+    a.a_m = f->a_m; a.a_s = f->a_s; a.a_yz = f->a_yz; a.a_lo = f->a_lo; a.a_hi = f->a_hi;
+    a.a_c1 = a.a_thr = 0;
+    a.a_hs = 0;
+    if (f->a_s < 0) {
+        const int nsh = -f->a_s;
+        if (nsh > 31) return (int)hipErrorInvalidValue;
+        a.a_c1 = (1LL << 30) + (1LL << (30 + nsh));
+        a.a_thr = 1LL << (30 + nsh);
+        a.a_hs = nsh - 1;
+    }
+    a.o_e = (int)off[0]; a.o_d = (int)off[1]; a.o_re = (int)off[2]; a.o_rd = (int)off[3]; a.o_rp = (int)off[4];
+    a.o_at = (int)off[5]; a.o_lut = (int)off[6]; a.o_po = (int)off[7]; a.o_tw = (int)off[8]; a.ks = f->ks;
+    // The dynamic-LDS ceiling is raised once per kernel (a host call that
+    // must not sit on every launch).
+    static int ceiling_set[2];
+    const int which = f->ks == 3 ? 0 : 1;
+    if (!ceiling_set[which]) {
+        const hipError_t e = which == 0 ? hipFuncSetAttribute((const void *)k_ib<3>,
+                                                              hipFuncAttributeMaxDynamicSharedMemorySize, IB_LDS_MAX)
+                                        : hipFuncSetAttribute((const void *)k_ib<5>,
+                                                              hipFuncAttributeMaxDynamicSharedMemorySize, IB_LDS_MAX);
+        if (e != hipSuccess) return uqk_fail(e);
+        ceiling_set[which] = 1;
+    }
+    hipStream_t st;
+    hipEvent_t e0, e1;
+    uqk_next_launch(&st, &e0, &e1);
+    const dim3 grid(images), block(64 * IB_WAVES);
+    if (which == 0) hipExtLaunchKernelGGL(k_ib<3>, grid, block, (uint32_t)lds, st, e0, e1, 0u, a);
+    else hipExtLaunchKernelGGL(k_ib<5>, grid, block, (uint32_t)lds, st, e0, e1, 0u, a);
+    const int rc = uqk_fail(hipGetLastError());
+    if (!rc) g_ib_launches++;
+    return rc;
+}

@@ -1897,270 +1897,6 @@ static int launch_dw_mfma(const UQKSpatial *d, const void *x, void *y, uint32_t 
     return 0;
 }
 
-// ---------------------------------------------------------------------------
-// Fused inverted bottleneck: 1x1 expand -> depthwise (stride 1) -> 1x1
-// project [-> residual add with the block input], one 16-wave workgroup per
-// image, every intermediate in LDS. Each phase is the arithmetic of the
-// separate kernels (same records, requantisation and post tables), so the
-// output is identical; only the HBM round trips of the expanded tensors go.
-//   LDS: X [P16][Cin] input | E [P16][Ce] expand out | D [P16][Ce] dw out |
-//        records (expand, dw, project) | dw tap words | add tables | tables
-// P16 = pixels rounded up to 16 (MFMA row tiles; rows past P are never
-// stored). The project output is staged in E (free by then) and written with
-// 16-byte stores.
-// ---------------------------------------------------------------------------
-struct IbArgs {
-    const int8_t *x;
-    int8_t *y;
-    int P, P16, H, W, Cin, Ce, Cout;
-    // expand (1x1): weights [Ce_pad][kpe], records, post table, requant mode
-    const int8_t *we;
-    const int4 *epi_e;
-    const uint8_t *lut_e;
-    int kpe, e_mode, e_yz, e_lo, e_hi;
-    // depthwise: tap words [ky][k][Ce], records, table, mode, zero points
-    const int4 *dww;
-    const int4 *epi_d;
-    const uint8_t *lut_d;
-    int d_mode, d_yz, d_lo, d_hi, d_xz, pt, pl;
-    // project (1x1)
-    const int8_t *wp;
-    const int4 *epi_p;
-    const uint8_t *lut_p;
-    int kpp, p_mode, p_yz, p_lo, p_hi;
-    // residual add (code 18): tables [2][256], operand order, requant
-    int has_add, add_x_first;
-    const int *add_tab;
-    int a_m, a_s, a_yz, a_lo, a_hi;
-    // LDS offsets (bytes)
-    int o_e, o_d, o_re, o_rd, o_rp, o_tw, o_at, o_lut;
-    int cq_magic;              // ceil(2^24 / (Ce / 4))
-    int w_magic;               // ceil(2^16 / W)
-};
-
-__device__ __forceinline__ int ib_requant(int acc, const Epi &e, int mode, int yz, int lo, int hi)
-{
-    switch (mode) {
-    case 0: return conv_requant<false, false>(acc, e, yz, lo, hi);
-    case 1: return conv_requant<true, false>(acc, e, yz, lo, hi);
-    case 2: return conv_requant<false, true>(acc, e, yz, lo, hi);
-    default: return conv_requant<true, true>(acc, e, yz, lo, hi);
-    }
-}
-
-__device__ __forceinline__ Epi ib_epi(const int8_t *smem, int off, int c)
-{
-    return load_epi((const int4 *)(smem + off), c);
-}
-
-// One 1x1 GEMM phase: A rows from LDS (row stride lda bytes, K = k_real
-// valid bytes, kpad columns), B = [n_pad][kpad] weights in HBM. Work items
-// are (row tile, group of NTG column tiles), spread over the 16 waves. The
-// requantised tile goes through `sink(row, col4, word)` as words of four
-// channels of one row.
-template <int NTG, typename Sink>
-__device__ __forceinline__ void ib_gemm(const int8_t *smem, const int8_t *A, int lda, int k_real, int kpad,
-                                        const int8_t *Bw, int ntiles, int mtiles, int epi_off, int mode, int yz, int lo,
-                                        int hi, const int8_t *lut, Sink sink)
-{
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int lr = lane & 15, lg = lane >> 4;
-    const int ngroups = (ntiles + NTG - 1) / NTG;
-    const int steps = kpad >> 6;
-    for (int item = wave; item < mtiles * ngroups; item += 16) {
-        const int mt = item / ngroups, ng = item - mt * ngroups;
-        const int nt0 = ng * NTG;
-        v4i acc[NTG];
-#pragma unroll
-        for (int j = 0; j < NTG; j++) acc[j] = (v4i){0, 0, 0, 0};
-        const int8_t *arow = A + (mt * 16 + lr) * lda + lg * 16;
-        for (int st = 0; st < steps; st++) {
-            const int k0 = st * 64 + lg * 16;
-            const v4i a = k0 < k_real ? *(const v4i *)(arow + st * 64) : (v4i){0, 0, 0, 0};
-#pragma unroll
-            for (int j = 0; j < NTG; j++) {
-                if (nt0 + j < ntiles) {
-                    const v4i b = *(const v4i *)(Bw + (long)((nt0 + j) * 16 + lr) * kpad + k0);
-                    acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[j], 0, 0, 0);
-                }
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < NTG; j++) {
-            if (nt0 + j >= ntiles) break;
-            const int col = (nt0 + j) * 16 + lr;
-            const Epi e = ib_epi(smem, epi_off, col);
-            int v[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                v[i] = ib_requant(acc[j][i], e, mode, yz, lo, hi);
-                if (lut) v[i] = (int)(signed char)lut[v[i] + 128];
-            }
-            const int word = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
-            sink(mt * 16 + lg * 4 + (lane & 3), (nt0 + j) * 16 + (lr & ~3), word);
-        }
-    }
-}
-
-template <int KS>
-__global__ __launch_bounds__(1024) void k_ib(IbArgs a)
-{
-    constexpr int NWK = KS > 4 ? 2 : 1;
-    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-    int8_t *X = smem, *E = smem + a.o_e, *D = smem + a.o_d;
-    const int tid = threadIdx.x;
-    const long n = blockIdx.x;
-    const int8_t *xin = a.x + n * a.P * a.Cin;
-
-    // Phase 0: image, records, tap words, tables into LDS.
-    for (int i = tid; i < (a.P * a.Cin) >> 4; i += 1024) ((v4i *)X)[i] = ((const v4i *)xin)[i];
-    for (int i = tid; i < 2 * a.Ce; i += 1024) {
-        ((int4 *)(smem + a.o_re))[i] = a.epi_e[i];
-        ((int4 *)(smem + a.o_rd))[i] = a.epi_d[i];
-    }
-    for (int i = tid; i < 2 * a.Cout; i += 1024) ((int4 *)(smem + a.o_rp))[i] = a.epi_p[i];
-    for (int i = tid; i < KS * NWK * a.Ce / 4; i += 1024) ((int4 *)(smem + a.o_tw))[i] = a.dww[i];
-    if (a.has_add) for (int i = tid; i < 512; i += 1024) ((int *)(smem + a.o_at))[i] = a.add_tab[i];
-    int8_t *lut_s = smem + a.o_lut;
-    if (tid < 64) {
-        if (a.lut_e) ((int *)lut_s)[tid] = ((const int *)a.lut_e)[tid];
-        if (a.lut_d) ((int *)(lut_s + 256))[tid] = ((const int *)a.lut_d)[tid];
-        if (a.lut_p) ((int *)(lut_s + 512))[tid] = ((const int *)a.lut_p)[tid];
-    }
-    __syncthreads();
-
-    // Phase 1: expand, E = requant(X * We).
-    const int mtiles = a.P16 >> 4;
-    ib_gemm<4>(smem, X, a.Cin, a.Cin, a.kpe, a.we, a.Ce >> 4, mtiles, a.o_re, a.e_mode, a.e_yz, a.e_lo, a.e_hi,
-               a.lut_e ? lut_s : nullptr,
-               [&](int row, int col, int word) { *(int *)(E + row * a.Ce + col) = word; });
-    __syncthreads();
-
-    // Phase 2: depthwise on E, four channels of one pixel per item; each
-    // kernel row's taps are windows of four adjacent columns (4x4 byte
-    // transpose of the column words), dotted with the row's tap words.
-    {
-        const int cq_n = a.Ce >> 2;
-        const int xzw = (a.d_xz & 0xff) * 0x01010101;
-        const int4 *tw = (const int4 *)(smem + a.o_tw);
-        for (int item = tid; item < a.P * cq_n; item += 1024) {
-            const int p = (int)(((unsigned long long)item * (unsigned)a.cq_magic) >> 24);
-            const int cq = item - p * cq_n;
-            const int y = (p * a.w_magic) >> 16, x = p - y * a.W;
-            int acc[4] = {0, 0, 0, 0};
-#pragma unroll
-            for (int ky = 0; ky < KS; ky++) {
-                const int iy = y + ky - a.pt;
-                const bool rowin = (unsigned)iy < (unsigned)a.H;
-#pragma unroll
-                for (int k = 0; k < NWK; k++) {
-                    int cw[4];
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const int ix = x - a.pl + 4 * k + j;
-                        cw[j] = rowin && (unsigned)ix < (unsigned)a.W ? *(const int *)(E + (iy * a.W + ix) * a.Ce + 4 * cq)
-                                                                       : xzw;
-                    }
-                    int w0, w1, w2, w3;
-                    transpose4x4(cw[0], cw[1], cw[2], cw[3], w0, w1, w2, w3);
-                    const int4 t = tw[(ky * NWK + k) * cq_n + cq];
-                    acc[0] = __builtin_amdgcn_sdot4(w0, t.x, acc[0], false);
-                    acc[1] = __builtin_amdgcn_sdot4(w1, t.y, acc[1], false);
-                    acc[2] = __builtin_amdgcn_sdot4(w2, t.z, acc[2], false);
-                    acc[3] = __builtin_amdgcn_sdot4(w3, t.w, acc[3], false);
-                }
-            }
-            int v[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const Epi e = ib_epi(smem, a.o_rd, 4 * cq + i);
-                v[i] = ib_requant(acc[i], e, a.d_mode, a.d_yz, a.d_lo, a.d_hi);
-                if (a.lut_d) v[i] = lut_s[256 + v[i] + 128];
-            }
-            *(int *)(D + p * a.Ce + 4 * cq) = pack4(v[0], v[1], v[2], v[3]);
-        }
-    }
-    __syncthreads();
-
-    // Phase 3: project (+ residual add), staged in E.
-    const int *at = (const int *)(smem + a.o_at);
-    ib_gemm<2>(smem, D, a.Ce, a.Ce, a.kpp, a.wp, a.Cout >> 4, mtiles, a.o_rp, a.p_mode, a.p_yz, a.p_lo, a.p_hi,
-               a.lut_p ? lut_s + 512 : nullptr, [&](int row, int col, int word) {
-                   if (row >= a.P) return;
-                   if (a.has_add) {
-                       const int xr = *(const int *)(X + row * a.Cin + col);
-                       int z[4];
-#pragma unroll
-                       for (int i = 0; i < 4; i++) {
-                           const int yv = sbyte(word, i), xv = sbyte(xr, i);
-                           const int av = a.add_x_first ? xv : yv, bv = a.add_x_first ? yv : xv;
-                           const int sum = at[av + 128] + at[256 + bv + 128];
-                           z[i] = min(max(uq_scale(sum, a.a_m, a.a_s) + a.a_yz, a.a_lo), a.a_hi);
-                       }
-                       word = pack4(z[0], z[1], z[2], z[3]);
-                   }
-                   *(int *)(E + row * a.Cout + col) = word;
-               });
-    __syncthreads();
-    int8_t *yout = a.y + n * a.P * a.Cout;
-    for (int i = tid; i < (a.P * a.Cout) >> 4; i += 1024) ((v4i *)yout)[i] = ((const v4i *)E)[i];
-}
-
-extern "C" size_t uqk_ib_lds(int P, int Cin, int Ce, int Cout, int ks, size_t *offsets)
-{
-    const int P16 = (P + 15) & ~15;
-    const int nwk = ks > 4 ? 2 : 1;
-    size_t o = 0, off[9];
-    off[0] = o; o += (size_t)P16 * Cin;                    // X
-    o = (o + 15) & ~(size_t)15; off[1] = o; o += (size_t)P16 * Ce;   // E (also the staged output)
-    o = (o + 15) & ~(size_t)15; off[2] = o; o += (size_t)P16 * Ce;   // D
-    o = (o + 15) & ~(size_t)15; off[3] = o; o += (size_t)Ce * 32;    // expand records
-    off[4] = o; o += (size_t)Ce * 32;                      // dw records
-    off[5] = o; o += (size_t)Cout * 32;                    // project records
-    off[6] = o; o += (size_t)ks * nwk * Ce * 4;            // tap words
-    o = (o + 15) & ~(size_t)15; off[7] = o; o += 512 * 4;  // add tables
-    off[8] = o; o += 3 * 256;                              // post tables
-    if (offsets) for (int i = 0; i < 9; i++) offsets[i] = off[i];
-    if ((size_t)P16 * Cout > (size_t)P16 * Ce) return 0;   // staged output must fit in E
-    return o;
-}
-
-extern "C" int uqk_ib(const UQKIb *f, const void *x, void *y, uint32_t images)
-{
-    if (!images) return 0;
-    IbArgs a;
-    size_t off[9];
-    const size_t lds = uqk_ib_lds(f->P, f->Cin, f->Ce, f->Cout, f->ks, off);
-    if (!lds || lds > 163840) return (int)hipErrorInvalidValue;
-    a.x = (const int8_t *)x; a.y = (int8_t *)y;
-    a.P = f->P; a.P16 = (f->P + 15) & ~15; a.H = f->H; a.W = f->W; a.Cin = f->Cin; a.Ce = f->Ce; a.Cout = f->Cout;
-    a.we = (const int8_t *)f->we; a.epi_e = (const int4 *)f->epi_e; a.lut_e = (const uint8_t *)f->lut_e;
-    a.kpe = f->kpe; a.e_mode = f->e_mode; a.e_yz = f->e_yz; a.e_lo = f->e_lo; a.e_hi = f->e_hi;
-    a.dww = (const int4 *)f->dww; a.epi_d = (const int4 *)f->epi_d; a.lut_d = (const uint8_t *)f->lut_d;
-    a.d_mode = f->d_mode; a.d_yz = f->d_yz; a.d_lo = f->d_lo; a.d_hi = f->d_hi; a.d_xz = f->d_xz; a.pt = f->pt; a.pl = f->pl;
-    a.wp = (const int8_t *)f->wp; a.epi_p = (const int4 *)f->epi_p; a.lut_p = (const uint8_t *)f->lut_p;
-    a.kpp = f->kpp; a.p_mode = f->p_mode; a.p_yz = f->p_yz; a.p_lo = f->p_lo; a.p_hi = f->p_hi;
-    a.has_add = f->has_add; a.add_x_first = f->add_x_first; a.add_tab = (const int *)f->add_tab;
-    a.a_m = f->a_m; a.a_s = f->a_s; a.a_yz = f->a_yz; a.a_lo = f->a_lo; a.a_hi = f->a_hi;
-    a.o_e = (int)off[1]; a.o_d = (int)off[2]; a.o_re = (int)off[3]; a.o_rd = (int)off[4]; a.o_rp = (int)off[5];
-    a.o_tw = (int)off[6]; a.o_at = (int)off[7]; a.o_lut = (int)off[8];
-    a.cq_magic = (int)((16777216u + (unsigned)(f->Ce / 4) - 1) / (unsigned)(f->Ce / 4));
-    a.w_magic = (65536 + f->W - 1) / f->W;
-    // The dynamic-LDS ceiling is raised once per kernel (a host call that
-    // must not sit on every launch).
-    static int ceiling_set[2];
-    const int which = f->ks == 3 ? 0 : 1;
-    if (!ceiling_set[which]) {
-        if (which == 0) UQK_TRY(hipFuncSetAttribute((const void *)k_ib<3>, hipFuncAttributeMaxDynamicSharedMemorySize, 163840));
-        else UQK_TRY(hipFuncSetAttribute((const void *)k_ib<5>, hipFuncAttributeMaxDynamicSharedMemorySize, 163840));
-        ceiling_set[which] = 1;
-    }
-    if (which == 0) UQK_LAUNCH(k_ib<3>, dim3(images), dim3(1024), lds, g_stream, a);
-    else UQK_LAUNCH(k_ib<5>, dim3(images), dim3(1024), lds, g_stream, a);
-    UQK_LAUNCHED();
-    return 0;
-}
-
 // Tile geometry for k_dw_tile; returns the dynamic LDS bytes, 0 if unsuited.
 static size_t dw_tile_plan(const UQKSpatial *d, uint32_t batches, DwTileArgs *t)
 {

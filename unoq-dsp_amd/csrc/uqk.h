@@ -59,9 +59,9 @@ size_t uqk_dw_win_lds(const UQKSpatial *d);
 void uqk_dw_band_prepare(UQKSpatial *d);
 int uqk_dw_band(const UQKSpatial *d, const void *x, void *y, uint32_t batches);
 
-/* Fused inverted bottleneck (1x1 expand -> stride-1 depthwise -> 1x1
- * project [-> residual add with the block input]), one workgroup per image.
- * Device tables are the three layers' own prepared tables. */
+/* Fused inverted bottleneck (ib.hip: 1x1 expand -> stride-1 depthwise ->
+ * 1x1 project [-> residual add with the block input]), one workgroup per
+ * image. Device tables are the three layers' own prepared tables. */
 typedef struct {
     int32_t P, H, W, Cin, Ce, Cout, ks, pt, pl;
     const void *we, *epi_e, *lut_e;
@@ -75,9 +75,9 @@ typedef struct {
     int32_t a_m, a_s, a_yz, a_lo, a_hi;
 } UQKIb;
 
-/* LDS bytes of the fused block for one image (0 if its staged output would
- * not fit); offsets[9] receives the region offsets when non-null. */
-size_t uqk_ib_lds(int P, int Cin, int Ce, int Cout, int ks, size_t *offsets);
+/* LDS bytes of the fused block for one image, 0 if the block does not fit
+ * the kernel; offsets[9] receives the region offsets when non-null. */
+size_t uqk_ib_lds(int P, int H, int W, int Cin, int Ce, int Cout, int ks, size_t *offsets);
 int uqk_ib(const UQKIb *f, const void *x, void *y, uint32_t images);
 
 /* Whether a conv layer fits the stem kernel (kh <= 4, kw * IC <= 16, no

@@ -65,9 +65,11 @@ def open_library(path=None):
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    # Test hook outside the plan ABI: launches of the large-tile GEMM.
-    lib.uqk_gemm_launches.restype = C.c_uint64
-    lib.uqk_gemm_launches.argtypes = []
+    # Test hooks outside the plan ABI: launches of the large-tile GEMM and of
+    # the fused bottleneck kernel.
+    for hook in ("uqk_gemm_launches", "uqk_ib_launches"):
+        getattr(lib, hook).restype = C.c_uint64
+        getattr(lib, hook).argtypes = []
     return lib
 
 
