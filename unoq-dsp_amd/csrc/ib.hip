@@ -1,5 +1,5 @@
 // Fused inverted bottleneck for gfx950: 1x1 expand -> stride-1 depthwise ->
-// 1x1 project [-> residual add with the block input], one workgroup of eight
+// 1x1 project [-> residual add with the block input], one workgroup of 16
 // waves per image, every intermediate in LDS (the reference runs the three
 // or four ops one after another through HBM: qnn.c:1074-1246 for the 1x1
 // convs, qnn.c:807-983 for the depthwise, qnn.c:1248-1290 for the add).
