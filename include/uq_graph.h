@@ -93,7 +93,11 @@ int ug_synchronize(void);
 /* All images of a tensor after the last run: bytes = images * tensor bytes
  * (for constants: the tensor bytes). Activation snapshots return 22 after a
  * ug_enqueue_device_noalloc run and once a caller buffer the last run was
- * bound to has been freed with ug_device_free. */
+ * bound to has been freed with ug_device_free. After a device-buffer run
+ * (ug_run_device, ug_enqueue_device) the output of a stem conv that ran
+ * fused with the 3x3 conv after it (it read the caller's input buffer and
+ * was never written) returns 22 too, from ug_snapshot as well; after a
+ * host-buffer run it is rebuilt from the library's copy of the input. */
 int ug_snapshot_images(uint32_t tensor, void *out, uint64_t bytes);
 
 /* No counterpart in the reference. For callers that cannot allocate device

@@ -496,3 +496,45 @@ def ib_plan(seed):
         z = p.add(x, z, act=_pick(rng, ["none", "relu", "relu6"])) if _pick(rng, [0, 1]) else \
             p.add(z, x, act=_pick(rng, ["none", "relu", "relu6"]))
     return p.build(z)
+
+
+def stem_conv_plan(seed):
+    """A stem conv (IC 1-4, 32 output channels) followed by a 3x3 stride-2
+    conv over its output, the pair the fused stem kernel takes: SAME or
+    explicit padding on both, strides 1-2 on the stem, widths from 16 to 96
+    input columns, odd heights, post tables, all requantisation ranges, and
+    sometimes an op after the pair."""
+    rng = Rng(seed, 929292)
+    p = Plan(seed)
+    ic = _pick(rng, [1, 2, 3, 3, 4])
+    w = _pick(rng, [16, 32, 48, 64, 96])
+    h = _pick(rng, [7, 9, 16, 23, 30])
+    x = p.input((1, h, w, ic), zp=int(rng.integers(1, -128, 127)[0]))
+    k = _pick(rng, [2, 3, 3, 4]) if ic < 4 else _pick(rng, [2, 3, 4])
+    stride = _pick(rng, [1, 2, 2])
+    lo = int(rng.integers(1, -24, -1)[0])
+
+    def layer(make):
+        for shift in ((lo, 3), (-12, -4), (-20, -1)):
+            try:
+                return make(shift)
+            except ValueError:
+                continue
+        raise AssertionError("unreachable")
+
+    def opts():
+        return dict(act=_pick(rng, ["none", "relu", "relu6"]), q6=int(rng.integers(1, 1, 200)[0]),
+                    lut=_random_lut(p, rng) if _pick(rng, [0, 0, 1]) else None, w_sigma=_pick(rng, [3, 40, 90]))
+    s = layer(lambda shift: p.conv(x, 32, k=k, stride=stride, padding=_pick(rng, ["same", (0, 0, 0, 0)]),
+                                   shift=shift, **opts()))
+    _, sh, sw, _ = p.shape(s)
+    if _pick(rng, [0, 1]) and sh >= 3 and sw >= 3:
+        padding = "same"
+    else:
+        pt, pb = _geometry(rng, sh, 3, 2, 1)
+        pl, pr = _geometry(rng, sw, 3, 2, 1)
+        padding = (pt, pl, pb, pr)
+    z = layer(lambda shift: p.conv(s, 32, k=3, stride=2, padding=padding, shift=shift, **opts()))
+    if _pick(rng, [0, 1]):
+        z = p.lut(z, _random_lut(p, rng))
+    return p.build(z)

@@ -13,7 +13,8 @@ import pytest
 import uq_plan as P
 import uq_workloads as W
 from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, dw_band_plan, dw_mfma_plan,
-                       gemm_plan, gemm_rows_plan, ib_plan, random_plan, pointwise_wide_plan, rows_conv_plan, stem_plan)
+                       gemm_plan, gemm_rows_plan, ib_plan, random_plan, pointwise_wide_plan, rows_conv_plan, stem_conv_plan,
+                       stem_plan)
 from test_oracle_vs_reference import (BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, softmax_table_plan,
                                       transpose_plan)
 from refs import oracle_run
@@ -300,6 +301,39 @@ def test_fused_bottleneck_plans(lib, monkeypatch, seed):
     before = lib.uqk_ib_launches()
     _assert_same(Graph(plan, lib).run_batch(x, images), want, f"unfused bottleneck plan {seed}")
     assert lib.uqk_ib_launches() == before
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_stem_conv_fusion(lib, monkeypatch, seed):
+    """A stem conv and the 3x3 stride-2 conv over its output run as one
+    launch by default: one to three images match the oracle byte for byte,
+    as they do unfused (UQ_FUSE_STEM=0). After a host-buffer run a snapshot
+    of the stem's output is rebuilt; after a device-buffer run (the stem
+    read the caller's buffer) it is refused with 22."""
+    plan = stem_conv_plan(seed)
+    images = 1 + seed % 3
+    x = P.random_input(plan, images, seed)
+    want = _oracle(plan, x, images)
+    g = Graph(plan, lib)
+    before = lib.uqk_stem_conv_launches()
+    _assert_same(g.run_batch(x, images), want, f"fused stem plan {seed}")
+    assert lib.uqk_stem_conv_launches() > before, "the fused stem kernel did not run"
+    stem_out = P.op_records(plan)[0][3]
+    nbytes = images * P.tensor_records(plan)[stem_out][1]
+    _, snap = oracle_run(plan, x, images, P.output_bytes(plan), snap=stem_out, snap_bytes=nbytes)
+    _assert_same(g.snapshot_images(stem_out, nbytes), snap, f"fused stem plan {seed}: stem output snapshot")
+    din, dout = DeviceBuffer(lib, x.nbytes), DeviceBuffer(lib, images * g.output_bytes)
+    din.upload(x)
+    assert lib.ug_run_device(din.ptr, dout.ptr, images) == 0
+    _assert_same(dout.download(), want, f"fused stem plan {seed}, device buffers")
+    buf = np.empty(nbytes, np.int8)
+    assert lib.ug_snapshot_images(stem_out, buf.ctypes.data, buf.nbytes) == 22
+    din.free()
+    dout.free()
+    monkeypatch.setenv("UQ_FUSE_STEM", "0")
+    before = lib.uqk_stem_conv_launches()
+    _assert_same(Graph(plan, lib).run_batch(x, images), want, f"unfused stem plan {seed}")
+    assert lib.uqk_stem_conv_launches() == before
 
 
 @pytest.mark.parametrize("seed", range(40))

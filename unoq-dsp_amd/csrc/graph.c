@@ -32,7 +32,8 @@ typedef struct { uint32_t offset, bytes, type, rank, d[4], flags, reserved[3]; }
 typedef struct { uint32_t code, a, b, out, p[4]; } Op;
 
 /* A fused group (see find_groups): an inverted bottleneck run by one launch
- * (kind 0), or a conv whose residual add runs in its epilogue (kind 1). */
+ * (kind 0), a conv whose residual add runs in its epilogue (kind 1), or a
+ * stem conv and the 3x3 stride-2 conv over its output (kind 2). */
 typedef struct {
     int kind;
     UQKIb desc;
@@ -41,6 +42,7 @@ typedef struct {
     uint32_t first, nops, in, out;
     const uint8_t *last_in;          /* input pointer of the last fused launch */
     uint32_t last_images;            /* images of that launch, 0 if not run fused since */
+    int last_ext;                    /* that launch read a caller buffer: inner tensors cannot be rebuilt */
 } Group;
 
 static struct {
@@ -885,6 +887,30 @@ static uint32_t find_bottleneck(uint32_t i, const uint16_t *users)
     return g->nops;
 }
 
+/* Stem + 3x3 stride 2: a stem conv (the stem form, 32 output channels)
+ * whose output, used by nothing else, is the input of the next op, a 3x3
+ * stride-2 conv over those 32 channels that fits stem.hip. On unless
+ * UQ_FUSE_STEM=0 at load time. */
+static int find_stem_conv(uint32_t i, const uint16_t *users)
+{
+    const Op *s = G.ops + i, *c = G.ops + i + 1;
+    if (s->code != 14 || c->code != 14 || c->a != s->out) return 0;
+    const uint32_t t = s->out;
+    if (users[t] != 1 || t == G.h.output || G.ts[s->a].rank != 4 || G.ts[s->a].d[0] != 1) return 0;
+    if (!uqk_stem_conv_ok(G.sp + i, G.sp + i + 1)) return 0;
+    Group *g = &G.groups[G.ngroups];
+    memset(g, 0, sizeof *g);
+    g->kind = 2;
+    g->first = i;
+    g->nops = 2;
+    g->in = s->a;
+    g->out = c->out;
+    G.fuse_at[i] = (uint16_t)(G.ngroups + 1);
+    G.fuse_of_tensor[t] = (uint16_t)(G.ngroups + 1);
+    G.ngroups++;
+    return 1;
+}
+
 static void find_groups(void)
 {
     static uint16_t users[UG_MAX_T];
@@ -897,8 +923,11 @@ static void find_groups(void)
     if (G.slices > UQK_MAX_SLICES) G.slices = UQK_MAX_SLICES;
     const char *env = getenv("UQ_FUSE_BOTTLENECK");
     const int bottleneck = !(env && !strcmp(env, "0"));
+    const char *senv = getenv("UQ_FUSE_STEM");
+    const int stem = !(senv && !strcmp(senv, "0"));
     for (uint32_t i = 0; i + 1 < G.h.no; i++) {
-        uint32_t n = bottleneck ? find_bottleneck(i, users) : 0;
+        uint32_t n = stem && find_stem_conv(i, users) ? 2 : 0;
+        if (!n && bottleneck) n = find_bottleneck(i, users);
         if (!n && find_conv_add(i, users)) n = 2;
         if (n) i += n - 1;
     }
@@ -913,6 +942,7 @@ static int materialize_group(uint32_t t)
     if (!gi) return 0;
     Group *g = &G.groups[gi - 1];
     if (!g->last_images) return 0;
+    if (g->last_ext) return 22;
     uint8_t *saved_in = G.ptr[g->in];
     G.ptr[g->in] = (uint8_t *)g->last_in;
     for (uint32_t k = 0; k < g->nops; k++) G.ptr[G.ops[g->first + k].out] = G.act[G.ops[g->first + k].out];
@@ -1030,23 +1060,30 @@ static int enqueue_range(uint32_t i0, uint32_t i1, uint32_t images, uint32_t *ne
     uint32_t i = i0;
     for (; i < i1; i++) {
         const uint32_t g = G.fuse_at[i];
-        /* A group runs fused only when the buffers it reads are the library's
-         * own, which still hold the same bytes if a snapshot later asks for
-         * an inner tensor (materialize_group). */
-        if (g && !G.profile_enabled && !G.ext[G.groups[g - 1].in] &&
-            (G.groups[g - 1].kind == 0 || !G.ext[G.groups[g - 1].res])) {
+        /* Groups of kind 0 and 1 run fused only when the buffers they read
+         * are the library's own, which still hold the same bytes if a
+         * snapshot later asks for an inner tensor (materialize_group). The
+         * stem group (kind 2) reads the plan input, a caller buffer on the
+         * device entry points: it runs fused on it, and its inner tensor's
+         * snapshot is then unavailable (22). */
+        if (g && !G.profile_enabled &&
+            (G.groups[g - 1].kind == 2 ||
+             (!G.ext[G.groups[g - 1].in] && (G.groups[g - 1].kind == 0 || !G.ext[G.groups[g - 1].res])))) {
             Group *grp = &G.groups[g - 1];
             int rc;
             if (grp->kind == 0) {
                 rc = uqk_ib(&grp->desc, G.ptr[grp->in], G.ptr[grp->out], images);
-            } else {
+            } else if (grp->kind == 1) {
                 grp->add.res = G.ptr[grp->res];
                 rc = uqk_conv_add(G.sp + i, G.ptr[grp->in], G.ptr[grp->out], images * G.ts[G.ops[i].a].d[0],
                                   &grp->add);
+            } else {
+                rc = uqk_stem_conv(G.sp + i, G.sp + i + 1, G.ptr[grp->in], G.ptr[grp->out], images);
             }
             if (rc) return rc;
             grp->last_in = G.ptr[grp->in];
             grp->last_images = images;
+            grp->last_ext = G.ext[grp->in];
             i += grp->nops - 1;
             continue;
         }
@@ -1665,7 +1702,9 @@ int ug_snapshot_images(uint32_t index, void *out, uint64_t bytes)
         return 0;
     }
     if (G.snap_void || !G.last_images || bytes != (uint64_t)G.last_images * t->bytes) return 22;
-    if (settle() || materialize_group(index)) return fail(24);
+    if (settle()) return fail(24);
+    const int mrc = materialize_group(index);
+    if (mrc) return mrc == 22 ? 22 : fail(24);
     if (uqk_d2h(out, G.ptr[index], bytes) || uqk_sync()) return fail(24);
     return 0;
 }
@@ -1683,7 +1722,9 @@ int ug_snapshot(uint32_t index, void *out, uint32_t bytes)
         memcpy(out, G.arena + t->offset, bytes); /* arena contents before any run */
         return 0;
     }
-    if (settle() || materialize_group(index)) return fail(24);
+    if (settle()) return fail(24);
+    const int mrc = materialize_group(index);
+    if (mrc) return mrc == 22 ? 22 : fail(24);
     if (uqk_d2h(out, G.ptr[index], bytes) || uqk_sync()) return fail(24);
     return 0;
 }

@@ -325,19 +325,6 @@ __device__ __forceinline__ void conv_store(const ConvArgs &a, const v4i (&acc)[R
     }
 }
 
-// 4x4 transpose of 16-lane rows across four registers: afterwards row j of
-// r[q] holds what row q of r[j] held. One v_permlane32_swap per register pair
-// exchanges the upper half of the first with the lower half of the second;
-// one v_permlane16_swap exchanges the odd rows of the first with the even
-// rows of the second.
-__device__ __forceinline__ void rows_transpose4(int (&r)[4])
-{
-    auto s02 = __builtin_amdgcn_permlane32_swap(r[0], r[2], false, false);
-    auto s13 = __builtin_amdgcn_permlane32_swap(r[1], r[3], false, false);
-    auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
-    auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
-    r[0] = (int)s01[0]; r[1] = (int)s01[1]; r[2] = (int)s23[0]; r[3] = (int)s23[1];
-}
 
 // Requantise and store a wave's tile computed with the channels as the MFMA
 // rows (weights in the A operand, pixels in B): a lane holds channels

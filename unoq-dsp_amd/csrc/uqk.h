@@ -80,6 +80,12 @@ typedef struct {
 size_t uqk_ib_lds(int P, int H, int W, int Cin, int Ce, int Cout, int ks, size_t *offsets);
 int uqk_ib(const UQKIb *f, const void *x, void *y, uint32_t images);
 
+/* Stem conv fused with the 3x3 stride-2 conv over its 32-channel output
+ * (stem.hip): whether the pair fits, and its launch (images of the stem's
+ * input to the 3x3's output). */
+int uqk_stem_conv_ok(const UQKSpatial *s, const UQKSpatial *c);
+int uqk_stem_conv(const UQKSpatial *s, const UQKSpatial *c, const void *x, void *y, uint32_t images);
+
 /* Whether a conv layer fits the stem kernel (kh <= 4, kw * IC <= 16, no
  * column dilation, left and right padding within 16 bytes, input rows a
  * multiple of 16 bytes, its staged rows within 48 KiB, OC % 16 == 0). Reads

@@ -125,6 +125,20 @@ __device__ __forceinline__ int quad_transpose_bytes(int w, int lane)
     return (int)__builtin_amdgcn_perm((unsigned)y, (unsigned)u, (j & 1) ? 0x03070105u : 0x06020400u);
 }
 
+// 4x4 transpose of 16-lane rows across four registers: afterwards row j of
+// r[q] holds what row q of r[j] held. One v_permlane32_swap per register pair
+// exchanges the upper half of the first with the lower half of the second;
+// one v_permlane16_swap exchanges the odd rows of the first with the even
+// rows of the second.
+__device__ __forceinline__ void rows_transpose4(int (&r)[4])
+{
+    auto s02 = __builtin_amdgcn_permlane32_swap(r[0], r[2], false, false);
+    auto s13 = __builtin_amdgcn_permlane32_swap(r[1], r[3], false, false);
+    auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+    auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+    r[0] = (int)s01[0]; r[1] = (int)s01[1]; r[2] = (int)s23[0]; r[3] = (int)s23[1];
+}
+
 // Sixteen bytes of value v at offset 16 * v: the source of staged chunks that
 // hold the input zero point (im2col padding), pixel chunks past K (whose
 // weights are zero, so any finite bytes do) and weight chunks past kpad (row
