@@ -20,9 +20,10 @@
 //      pixels of one channel into four channels of one pixel: 4-byte LDS
 //      writes into the window plane of the channels' 16-channel group, at
 //      the pixel's padded position.
-//   2  depthwise on the matrix cores as in k_dw_mfma: per 16 pixels x 16
-//      channels, one v_mfma_i32_16x16x64_i8 per four taps, whose A rows are
-//      16-byte reads of the window planes and whose B is block diagonal (a
+//   2  depthwise on the matrix cores: 3x3 on 32x32 tiles, one
+//      v_mfma_i32_32x32x32_i8 per tap (ib_dw3_32); 5x5 as in k_dw_mfma, per
+//      16 pixels x 16 channels one v_mfma_i32_16x16x64_i8 per four taps. The
+//      A rows are 16-byte reads of the window planes, B is block diagonal (a
 //      lane's tap weight at its channel's byte). Output rows of Ce bytes
 //      (padded by 16) in LDS.
 //   3  project: 16x16 tiles on v_mfma_i32_16x16x64_i8 (finer work items for
@@ -302,6 +303,70 @@ __device__ __forceinline__ void ib_dw(const IbArgs &a, const int8_t *smem, const
     }
 }
 
+// The 3x3 depthwise on 32x32 tiles (v_mfma_i32_32x32x32_i8, one per tap):
+// 32 pixels (rows: 16-byte reads of the window planes of the tile's two
+// 16-channel groups) by 32 channels (columns: block-diagonal, lane (channel
+// n, half h) holds w[tap][n] in byte n % 16 of the half that contains n).
+// A lane's 16 results share one channel, so one record per lane, and the
+// epilogue is the expand's: 4x4 byte transposes into 4-byte writes of D.
+// Items (32-channel tile, 32-pixel tile), channel tile major; the taps'
+// operands and the record are rebuilt when the channel tile changes.
+template <bool HI, bool CORR, bool LUT>
+__device__ __forceinline__ void ib_dw3_32(const IbArgs &a, const int8_t *smem, const int8_t *E, int8_t *D,
+                                          const int8_t *lut_s, const int *padoff, const int *tw, int plane)
+{
+    const int lane = threadIdx.x & 63;
+    const int fr = lane & 31, fh = lane >> 5;
+    const int ptiles = (a.P + 31) >> 5;
+    int i0, i1;
+    ib_items(a.Ce >> 5, a.P, i0, i1);
+    const int vlo = vgpr(a.d_lo), vhi = vgpr(a.d_hi);
+    const int corner = a.pt * a.cols_p + a.pl;
+    int off[9];
+#pragma unroll
+    for (int t = 0; t < 9; t++) off[t] = ((t / 3) * a.cols_p + t % 3) * 16;
+    v4i B[9];
+    Epi e = {};
+    int loaded = -1;
+    const int8_t *gplane = E;
+    int ct = i0 / ptiles, pt = i0 - ct * ptiles;
+    for (int item = i0; item < i1; item++, pt = pt + 1 < ptiles ? pt + 1 : 0, ct += pt == 0) {
+        if (ct != loaded) {
+            const int c = ct * 32 + fr, q = (fr & 15) >> 2;
+            const bool mine = (fr >> 4) == fh;
+#pragma unroll
+            for (int t = 0; t < 9; t++) {
+                const int wb = mine ? (tw[(t / 3) * a.Ce + c] >> (8 * (t % 3))) & 0xff : 0;
+                const int word = wb << (8 * (fr & 3));
+                B[t] = (v4i){q == 0 ? word : 0, q == 1 ? word : 0, q == 2 ? word : 0, q == 3 ? word : 0};
+            }
+            e = load_epi((const int4 *)(smem + a.o_rd), c);
+            gplane = E + ((ct * 2 + fh) * plane - corner) * 16;
+            loaded = ct;
+        }
+        const int8_t *base = gplane + padoff[min(pt * 32 + fr, a.P - 1)] * 16;
+        v16i acc;
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[r] = 0;
+#pragma unroll
+        for (int t = 0; t < 9; t++) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i *)(base + off[t]), B[t], acc, 0, 0, 0);
+        // acc[4g + i]: pixel pt*32 + 8g + 4fh + i, channel ct*32 + fr.
+        const int c = ct * 32 + (fr & ~3);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            int v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[i] = conv_requant<HI, CORR>(acc[4 * g + i], e, a.d_yz, vlo, vhi);
+                if (LUT) v[i] = lut_s[256 + v[i] + 128];
+            }
+            const int word = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
+            const int px = pt * 32 + 8 * g + 4 * fh + (lane & 3);
+            if (px < a.P) *(int *)(D + __mul24(px, a.ds) + c) = word;
+        }
+    }
+}
+
 template <int KS>
 __global__ __launch_bounds__(64 * IB_WAVES) void k_ib(IbArgs a)
 {
@@ -358,7 +423,11 @@ __global__ __launch_bounds__(64 * IB_WAVES) void k_ib(IbArgs a)
     __syncthreads();
 
     // Phase 2: depthwise into D.
-#define IB_DW(H, C, L) ib_dw<KS, H, C, L>(a, smem, E, D, lut_s, padoff, tw, plane)
+#define IB_DW(H, C, L)                                                   \
+    do {                                                                 \
+        if (KS == 3) ib_dw3_32<H, C, L>(a, smem, E, D, lut_s, padoff, tw, plane); \
+        else ib_dw<KS, H, C, L>(a, smem, E, D, lut_s, padoff, tw, plane); \
+    } while (0)
     switch (a.d_mode * 2 + (a.lut_d != nullptr)) {
     case 0: IB_DW(false, false, false); break;
     case 1: IB_DW(false, false, true); break;
