@@ -498,6 +498,148 @@ def ib_plan(seed):
     return p.build(z)
 
 
+def uib_lds(H, W, Ho, Wo, cin, ce, cout, k0, k, s, add, R):
+    """LDS bytes of the banded bottleneck kernel's workgroup for bands of R
+    output rows (its layout: staged input, start-depthwise rows, window
+    planes, depthwise rows, records, tables, position tables, tap words), 0
+    when over 160 KiB or when the output stage does not fit."""
+    def up(v):
+        return (v + 15) & ~15
+    re = (R - 1) * s + k if k else R
+    rv = min(re, H)
+    pe, po = rv * W, R * Wo
+    cols0, cols_p = W + k0 - 1, ((Wo - 1) * s + k if k else 0)
+    o = up((cin // 16) * (rv + k0 - 1) * cols0 * 16 if k0 else pe * (cin + 16))
+    x1 = o
+    o += up(pe * (cin + 16) if k0 else 0)
+    e = o
+    o += up((ce // 16) * re * cols_p * 16 if k else 0)
+    d = o
+    o += up((po if k else pe) * (ce + 16)) + 64
+    o += (cin * 32 if k0 else 0) + ce * 32 + (ce * 32 if k else 0) + cout * 32 + (2048 if add else 0) + 1024
+    o += up(pe * 4 if k0 else 0) + up(pe * 4 if k else 0) + up(po * 4 if k else 0) + up(po * 4 if add else 0)
+    o += up(k0 * (2 if k0 > 4 else 1) * cin * 4) + up(k * (2 if k > 4 else 1) * ce * 4)
+    if po * cout > ((d - e) if k else (e - x1)):
+        return 0
+    return o if o <= 163840 else 0
+
+
+def dw_window_form(c, oh, ow, k, s):
+    """Whether the library keeps a depthwise layer in window form (tap words
+    [ky][k > 4 ? 2 : 1][C], the form the fused kernels read): the dot4
+    window kernel's plan must fit its 64 KiB of LDS."""
+    if c % 4 or k not in (3, 5) or s not in (1, 2):
+        return False
+    c4, cq = c // 4, 1
+    while cq < 16 and c4 % (2 * cq) == 0:
+        cq *= 2
+    xq_all = (ow + 3) // 4
+    tiles_x = (xq_all + 7) // 8
+    xw = (xq_all + tiles_x - 1) // tiles_x
+    if xw >= 4 and cq > 4:
+        cq = 4
+    th = 256 // (xw * cq)
+    if th < 1:
+        return False
+    ir = (min(th, oh) - 1) * s + k
+    njq = (4 * xw + (4 // s if k > 4 else 0) + 3) // 4
+    if ir * njq >= 65536 // njq:
+        return False
+    return ir * njq * cq * 5 * 16 + k * (2 if k > 4 else 1) * cq * 16 + cq * 4 * 32 + 256 <= 65536
+
+
+def uib_rows(H, W, Ho, Wo, cin, ce, cout, k0, k, s, add):
+    """Output rows per band the banded bottleneck kernel takes: the most
+    whose workgroup fits (0: none does)."""
+    for R in range(Ho, 0, -1):
+        if uib_lds(H, W, Ho, Wo, cin, ce, cout, k0, k, s, add, R):
+            return R
+    return 0
+
+
+def uib_plan(seed):
+    """uib_block's plan."""
+    return uib_block(seed)[0]
+
+
+def uib_block(seed):
+    """(plan, rows, out_rows): a universal inverted bottleneck of the shapes the banded fused kernel
+    takes (behind a post table, so that the block input is the library's own
+    buffer): a 3x3 or 5x5 stride-1 start depthwise (SAME, or explicit pads
+    that keep the map), 1x1 expand, a 3x3 or 5x5 depthwise of stride 1 or 2
+    (SAME or explicit pads), 1x1 project, and a residual add with the block
+    input (either operand order) at stride 1 when the channel counts match;
+    blocks without the start depthwise (then at stride 2) or without the
+    second one; non-square maps from 3 to 30 rows, one band to many, post
+    tables, activations and all requantisation ranges. Both depthwise layers
+    in window form (dw_window_form), which the fused kernels need. rows: the
+    output rows per band the kernel takes (uib_rows); out_rows: the block's
+    output rows."""
+    rng = Rng(seed, 626262)
+    p = Plan(seed)
+
+    def pads(k):
+        if _pick(rng, [0, 1]):
+            return "same"
+        pt, pl = int(rng.integers(1, 0, k - 1)[0]), int(rng.integers(1, 0, k - 1)[0])
+        return (pt, pl, k - 1 - pt, k - 1 - pl)
+
+    while True:
+        form = _pick(rng, ["both", "both", "start", "mid"])
+        h, w = int(_pick(rng, [3, 5, 7, 9, 14, 17, 28, 30])), int(_pick(rng, [3, 5, 7, 14, 16, 28]))
+        cin = int(_pick(rng, [32, 64, 96, 128]))
+        ce = int(_pick(rng, [64, 96, 128, 192, 256, 384, 512]))
+        k0 = int(_pick(rng, [3, 5])) if form != "mid" else 0
+        k = int(_pick(rng, [3, 5])) if form != "start" else 0
+        s = 2 if form == "mid" else (int(_pick(rng, [1, 2])) if k else 1)
+        add = s == 1 and bool(_pick(rng, [0, 1, 1]))
+        cout = cin if add else int(_pick(rng, [32, 64, 96, 128]))
+        pad0 = pads(k0) if k0 else None
+        pad = (pads(k) if s == 1 else _pick(rng, ["same", (0, 0, 0, 0), (1, 1, 1, 1)])) if k else None
+        if k:
+            if pad == "same":
+                ho, wo = -(-h // s), -(-w // s)
+            else:
+                ho, wo = (h + pad[0] + pad[2] - k) // s + 1, (w + pad[1] + pad[3] - k) // s + 1
+            if ho < 1 or wo < 1 or (s == 1 and (ho, wo) != (h, w)):
+                continue
+        else:
+            ho, wo = h, w
+        if (k0 and not dw_window_form(cin, h, w, k0, 1)) or (k and not dw_window_form(ce, ho, wo, k, s)):
+            continue
+        rows = uib_rows(h, w, ho, wo, cin, ce, cout, k0, k, s, add)
+        if rows:
+            break
+    x = p.input((1, h, w, cin), zp=int(rng.integers(1, -128, 127)[0]))
+    x = p.lut(x, _random_lut(p, rng))
+
+    def layer(make):
+        lo = int(rng.integers(1, -24, -1)[0])
+        for shift in ((lo, 3), (-12, -4), (-20, -1)):
+            try:
+                return make(shift)
+            except ValueError:
+                continue
+        raise AssertionError("unreachable")
+
+    def opts():
+        return dict(act=_pick(rng, ["none", "relu", "relu6"]), q6=int(rng.integers(1, 1, 200)[0]),
+                    lut=_random_lut(p, rng) if _pick(rng, [0, 0, 1]) else None, w_sigma=_pick(rng, [3, 40, 90]))
+    y = x
+    if k0:
+        y = layer(lambda shift: p.depthwise(y, k=k0, stride=1, padding=pad0, shift=shift,
+                                             bias_sigma=_pick(rng, [0, 2048, 60000]), **opts()))
+    e = layer(lambda shift: p.conv(y, ce, k=1, shift=shift, **opts()))
+    if k:
+        e = layer(lambda shift: p.depthwise(e, k=k, stride=s, padding=pad, shift=shift,
+                                             bias_sigma=_pick(rng, [0, 2048, 60000]), **opts()))
+    z = layer(lambda shift: p.conv(e, cout, k=1, shift=shift, **opts()))
+    if add:
+        z = p.add(x, z, act=_pick(rng, ["none", "relu", "relu6"])) if _pick(rng, [0, 1]) else \
+            p.add(z, x, act=_pick(rng, ["none", "relu", "relu6"]))
+    return p.build(z), rows, ho
+
+
 def stem_conv_plan(seed):
     """A stem conv (IC 1-4, 32 output channels) followed by a 3x3 stride-2
     conv over its output, the pair the fused stem kernel takes: SAME or

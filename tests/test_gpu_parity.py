@@ -14,7 +14,7 @@ import uq_plan as P
 import uq_workloads as W
 from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, dw_band_plan, dw_mfma_plan,
                        gemm_plan, gemm_rows_plan, ib_plan, random_plan, pointwise_wide_plan, rows_conv_plan, stem_conv_plan,
-                       stem_plan)
+                       stem_plan, uib_block)
 from test_oracle_vs_reference import (BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, softmax_table_plan,
                                       transpose_plan)
 from refs import oracle_run
@@ -304,6 +304,55 @@ def test_fused_bottleneck_plans(lib, monkeypatch, seed):
 
 
 @pytest.mark.parametrize("seed", range(40))
+def test_banded_bottleneck_plans(lib, monkeypatch, seed):
+    """Random universal inverted bottlenecks (a start depthwise and/or a
+    stride-1 or stride-2 depthwise between the two 1x1 convs, an optional
+    add) run as one banded launch: the kernel runs, one to three images
+    match the oracle byte for byte, as they do unfused (UQ_FUSE_UIB=0), and a
+    snapshot of the block's first inner tensor is rebuilt from the block
+    input. UQ_FUSE_UIB=2 fuses blocks of several bands too; by default only
+    single-band blocks run fused (or, when the whole block needs several
+    bands, possibly its part after the start depthwise), with the same
+    bytes."""
+    plan, rows, out_rows = uib_block(seed)
+    monkeypatch.setenv("UQ_FUSE_UIB", "2")
+    images = 1 + seed % 3
+    x = P.random_input(plan, images, seed)
+    want = _oracle(plan, x, images)
+    g = Graph(plan, lib)
+    before = lib.uqk_uib_launches()
+    _assert_same(g.run_batch(x, images), want, f"banded bottleneck plan {seed}")
+    assert lib.uqk_uib_launches() > before, "the banded bottleneck kernel did not run"
+    inner = P.op_records(plan)[1][3]            # op 0 is the post table in front of the block
+    nbytes = images * P.tensor_records(plan)[inner][1]
+    _, snap = oracle_run(plan, x, images, P.output_bytes(plan), snap=inner, snap_bytes=nbytes)
+    _assert_same(g.snapshot_images(inner, nbytes), snap, f"banded bottleneck plan {seed}: inner snapshot")
+    monkeypatch.delenv("UQ_FUSE_UIB")
+    before = lib.uqk_uib_launches()
+    _assert_same(Graph(plan, lib).run_batch(x, images), want, f"default banded bottleneck plan {seed}")
+    if rows == out_rows:
+        assert lib.uqk_uib_launches() > before, "a single-band block did not run fused by default"
+    monkeypatch.setenv("UQ_FUSE_UIB", "0")
+    before = lib.uqk_uib_launches()
+    _assert_same(Graph(plan, lib).run_batch(x, images), want, f"unfused banded bottleneck plan {seed}")
+    assert lib.uqk_uib_launches() == before
+
+
+@pytest.mark.parametrize("mode,launches", [("1", 1), ("2", 3)])
+def test_mnv4_banded_groups(lib, monkeypatch, mode, launches):
+    """MobileNetV4's 14x14 ExtraDW block runs on the banded kernel in one
+    band by default; with UQ_FUSE_UIB=2 its 28x28 block with a stride-2
+    depthwise (five bands) and its 7x7 ExtraDW block (two bands) do too; the
+    bytes match the oracle either way (batch 3, one image slice)."""
+    monkeypatch.setenv("UQ_FUSE_UIB", mode)
+    plan, _ = W.mnv4()
+    x = P.random_input(plan, 3, 77)
+    before = lib.uqk_uib_launches()
+    _assert_same(Graph(plan, lib).run_batch(x, 3), _oracle(plan, x, 3), "mnv4 with banded groups")
+    assert lib.uqk_uib_launches() - before == launches
+
+
+@pytest.mark.parametrize("seed", range(40))
 def test_stem_conv_fusion(lib, monkeypatch, seed):
     """A stem conv and the 3x3 stride-2 conv over its output run as one
     launch by default: one to three images match the oracle byte for byte,
@@ -468,9 +517,9 @@ def test_split_batches_continue_across_calls(lib, monkeypatch):
 @pytest.mark.parametrize("images", [3, 130])
 def test_device_path_output_reshape(lib, images):
     """MobileNetV4 ends in a reshape (op 5) of the classifier's output, which
-    on the device path lands in the caller's buffer: the output and a
-    snapshot of the reshaped tensor match the oracle, on one stream and on
-    two slices."""
+    on the device path lands in the caller's buffer (the classifier writes
+    it there, the reshape moves nothing): the output and a snapshot of the
+    reshaped tensor match the oracle, on one stream and on two slices."""
     plan, _ = W.mnv4()
     ops, recs = P.op_records(plan), P.tensor_records(plan)
     out = struct.unpack_from("<I", plan, 24)[0]          # header: output tensor index
@@ -486,9 +535,8 @@ def test_device_path_output_reshape(lib, images):
     y = dout.download()
     for j in (0, images // 2, images - 1):
         _assert_same(y[j * ob:(j + 1) * ob], _oracle(plan, x[j * ib:(j + 1) * ib], 1), f"image {j}")
-    if images <= 3:
-        _, want = oracle_run(plan, x, images, P.output_bytes(plan), snap=src, snap_bytes=images * recs[src][1])
-        _assert_same(g.snapshot_images(src, images * recs[src][1]), want, f"snapshot of tensor {src}")
+    _, want = oracle_run(plan, x, images, P.output_bytes(plan), snap=src, snap_bytes=images * recs[src][1])
+    _assert_same(g.snapshot_images(src, images * recs[src][1]), want, f"snapshot of tensor {src}")
     din.free()
     dout.free()
 

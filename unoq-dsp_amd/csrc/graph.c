@@ -32,11 +32,13 @@ typedef struct { uint32_t offset, bytes, type, rank, d[4], flags, reserved[3]; }
 typedef struct { uint32_t code, a, b, out, p[4]; } Op;
 
 /* A fused group (see find_groups): an inverted bottleneck run by one launch
- * (kind 0), a conv whose residual add runs in its epilogue (kind 1), or a
- * stem conv and the 3x3 stride-2 conv over its output (kind 2). */
+ * (kind 0), a conv whose residual add runs in its epilogue (kind 1), a stem
+ * conv and the 3x3 stride-2 conv over its output (kind 2), or a banded
+ * universal inverted bottleneck (kind 3). */
 typedef struct {
     int kind;
     UQKIb desc;
+    UQKUib ub;                       /* kind 3 */
     UQKAdd add;                      /* kind 1; add.res is set per launch */
     uint32_t res;                    /* kind 1: tensor of the add's other operand */
     uint32_t first, nops, in, out;
@@ -66,6 +68,10 @@ static struct {
     uint16_t fuse_at[UG_MAX_OP];
     uint16_t fuse_of_tensor[UG_MAX_T];   /* group index + 1 of an inner tensor */
     uint8_t ext[UG_MAX_T];               /* G.ptr[t] is a caller buffer this run */
+    /* fwd[i]: op i's output is used only by op i + 1, a reshape (code 5) to
+     * the graph output; when that output is a caller buffer, op i writes
+     * its bytes there directly and the reshape moves nothing. */
+    uint8_t fwd[UG_MAX_OP];
     int slices;                          /* UQ_STREAMS at load: image slices of a batch, 0 = default */
     int split_open, split_n;             /* the last split batch's side stream is not joined yet */
     uint32_t split_images;               /* ... its image count, input and output addresses */
@@ -887,6 +893,99 @@ static uint32_t find_bottleneck(uint32_t i, const uint16_t *users)
     return g->nops;
 }
 
+/* Universal inverted bottlenecks by bands of output rows (uib.hip): a
+ * stride-1 depthwise whose output keeps the map size and feeds only a 1x1
+ * conv (the start depthwise), then [a depthwise of stride 1 or 2], then a
+ * 1x1 conv, optionally followed by an add of the block input; or a 1x1 conv,
+ * a stride-2 depthwise and a 1x1 conv (k_ib takes the stride-1 form). The
+ * depthwise layers in window form; inner tensors single-use activations,
+ * not the plan output; one image per plan image.
+ *
+ * By default only blocks whose whole map fits one workgroup (one band) run
+ * fused: on MobileNetV4-S at batch 256 that fuses the 14x14 ExtraDW block
+ * (0.437 against 0.457 ms per step unfused), while the banded forms measured
+ * slower than their separate launches (the 28x28 block in five bands of
+ * three rows, 0.471 ms with it; the 7x7 ExtraDW block in two bands, 0.463).
+ * UQ_FUSE_UIB=2 at load time fuses banded blocks too, =0 none. */
+static uint32_t find_uib(uint32_t i, const uint16_t *users, int bands_ok)
+{
+    UQKUib u;
+    memset(&u, 0, sizeof u);
+    uint32_t j = i;
+    const Tensor *x = G.ts + G.ops[i].a;
+    if (x->flags || x->rank != 4 || x->d[0] != 1 || G.ops[i].a == G.h.input) return 0;
+    if (G.ops[j].code == 15) {
+        const UQKSpatial *d = G.sp + j;
+        if (!d->dwwin || d->sh != 1 || d->sw != 1 || d->oh != d->ih || d->ow != d->iw || d->oc != d->ic) return 0;
+        u.k0 = d->kh; u.p0t = d->pt; u.p0l = d->pl;
+        u.dw0 = d->wdot; u.epi0 = d->epi; u.lut0 = d->lut;
+        u.m0 = (d->hi_shift ? 1 : 0) | (d->corr ? 2 : 0); u.yz0 = d->yz; u.lo0 = d->lo; u.hi0 = d->hi; u.xz0 = d->xz;
+        j++;
+    }
+    if (j + 1 >= G.h.no || !pointwise_conv(j) || G.ops[j].a != (j > i ? G.ops[j - 1].out : G.ops[i].a)) return 0;
+    const UQKSpatial *se = G.sp + j;
+    if (u.k0 && (se->ih != G.sp[i].oh || se->iw != G.sp[i].ow || se->ic != G.sp[i].oc)) return 0;
+    u.H = se->ih; u.W = se->iw; u.Cin = se->ic; u.Ce = se->oc;
+    u.we = se->w; u.epi_e = se->epi; u.lut_e = se->lut; u.kpe = se->kpad;
+    u.e_mode = (se->hi_shift ? 1 : 0) | (se->corr ? 2 : 0); u.e_yz = se->yz; u.e_lo = se->lo; u.e_hi = se->hi;
+    j++;
+    if (G.ops[j].code == 15) {
+        const UQKSpatial *d = G.sp + j;
+        if (!d->dwwin || d->sh != d->sw || d->ih != u.H || d->iw != u.W || d->ic != u.Ce || d->oc != u.Ce ||
+            G.ops[j].a != G.ops[j - 1].out)
+            return 0;
+        u.k = d->kh; u.s = d->sh; u.pt = d->pt; u.pl = d->pl;
+        u.dww = d->wdot; u.epi_d = d->epi; u.lut_d = d->lut;
+        u.d_mode = (d->hi_shift ? 1 : 0) | (d->corr ? 2 : 0); u.d_yz = d->yz; u.d_lo = d->lo; u.d_hi = d->hi;
+        u.d_xz = d->xz;
+        u.Ho = d->oh; u.Wo = d->ow;
+        j++;
+    } else {
+        u.Ho = u.H; u.Wo = u.W;
+    }
+    if (j >= G.h.no || !pointwise_conv(j) || G.ops[j].a != G.ops[j - 1].out) return 0;
+    if (!u.k0 && (!u.k || u.s == 1)) return 0;
+    const UQKSpatial *sp = G.sp + j;
+    if (sp->ih != u.Ho || sp->iw != u.Wo || sp->ic != u.Ce) return 0;
+    u.Cout = sp->oc;
+    u.wp = sp->w; u.epi_p = sp->epi; u.lut_p = sp->lut; u.kpp = sp->kpad;
+    u.p_mode = (sp->hi_shift ? 1 : 0) | (sp->corr ? 2 : 0); u.p_yz = sp->yz; u.p_lo = sp->lo; u.p_hi = sp->hi;
+    for (uint32_t k = i; k < j; k++)
+        if (users[G.ops[k].out] != 1 || G.ops[k].out == G.h.output) return 0;
+    uint32_t nops = j - i + 1, out = G.ops[j].out;
+    if (j + 1 < G.h.no && G.ops[j + 1].code == 18) {
+        const Op *ad = G.ops + j + 1;
+        const uint32_t xin = G.ops[i].a;
+        const int ordered = ad->a == xin && ad->b == out, swapped = ad->a == out && ad->b == xin;
+        const int32_t *q = (const int32_t *)(G.arena + G.ts[ad->p[0]].offset);
+        /* The fused add takes shifts in [-31, 31] (its rescale as one
+         * multiply-add); others leave the add to its own launch. */
+        if ((ordered || swapped) && users[out] == 1 && out != G.h.output && u.Cin == u.Cout && u.Ho == u.H &&
+            u.Wo == u.W && q[1] >= -31 && q[1] <= 31) {
+            u.has_add = 1;
+            u.add_x_first = ordered;
+            u.add_tab = G.dev_arena + G.ts[ad->p[0]].offset + 8 * 4;
+            u.a_m = q[0]; u.a_s = q[1]; u.a_yz = q[2]; u.a_lo = q[3]; u.a_hi = q[4];
+            nops++;
+            out = ad->out;
+        }
+    }
+    if (!uqk_uib_plan(&u)) return 0;
+    if (bands_ok < 2 && u.R < u.Ho) return 0;
+    Group *g = &G.groups[G.ngroups];
+    memset(g, 0, sizeof *g);
+    g->kind = 3;
+    g->ub = u;
+    g->first = i;
+    g->nops = nops;
+    g->in = G.ops[i].a;
+    g->out = out;
+    G.fuse_at[i] = (uint16_t)(G.ngroups + 1);
+    for (uint32_t k = i; k + 1 < i + nops; k++) G.fuse_of_tensor[G.ops[k].out] = (uint16_t)(G.ngroups + 1);
+    G.ngroups++;
+    return nops;
+}
+
 /* Stem + 3x3 stride 2: a stem conv (the stem form, 32 output channels)
  * whose output, used by nothing else, is the input of the next op, a 3x3
  * stride-2 conv over those 32 channels that fits stem.hip. On unless
@@ -925,11 +1024,26 @@ static void find_groups(void)
     const int bottleneck = !(env && !strcmp(env, "0"));
     const char *senv = getenv("UQ_FUSE_STEM");
     const int stem = !(senv && !strcmp(senv, "0"));
+    const char *uenv = getenv("UQ_FUSE_UIB");
+    const int uib = !uenv ? 1 : !strcmp(uenv, "0") ? 0 : !strcmp(uenv, "2") ? 2 : 1;
     for (uint32_t i = 0; i + 1 < G.h.no; i++) {
         uint32_t n = stem && find_stem_conv(i, users) ? 2 : 0;
+        if (!n && uib) n = find_uib(i, users, uib);
         if (!n && bottleneck) n = find_bottleneck(i, users);
         if (!n && find_conv_add(i, users)) n = 2;
         if (n) i += n - 1;
+    }
+    memset(G.fwd, 0, sizeof G.fwd);
+    for (uint32_t i = 1; i < G.h.no; i++) {
+        const Op *r = G.ops + i, *p = G.ops + i - 1;
+        const uint32_t t = r->a;
+        if (r->code != 5 || r->out != G.h.output || p->out != t || users[t] != 1 || t == G.h.input ||
+            G.ts[t].flags || G.ts[r->out].flags || G.ts[t].bytes != G.ts[r->out].bytes)
+            continue;
+        int grouped = 0;
+        for (uint32_t g = 0; g < G.ngroups; g++)
+            if (i - 1 >= G.groups[g].first && i - 1 < G.groups[g].first + G.groups[g].nops) grouped = 1;
+        if (!grouped) G.fwd[i - 1] = 1;
     }
 }
 
@@ -1060,7 +1174,7 @@ static int enqueue_range(uint32_t i0, uint32_t i1, uint32_t images, uint32_t *ne
     uint32_t i = i0;
     for (; i < i1; i++) {
         const uint32_t g = G.fuse_at[i];
-        /* Groups of kind 0 and 1 run fused only when the buffers they read
+        /* Groups of kinds 0, 1 and 3 run fused only when the buffers they read
          * are the library's own, which still hold the same bytes if a
          * snapshot later asks for an inner tensor (materialize_group). The
          * stem group (kind 2) reads the plan input, a caller buffer on the
@@ -1068,11 +1182,13 @@ static int enqueue_range(uint32_t i0, uint32_t i1, uint32_t images, uint32_t *ne
          * snapshot is then unavailable (22). */
         if (g && !G.profile_enabled &&
             (G.groups[g - 1].kind == 2 ||
-             (!G.ext[G.groups[g - 1].in] && (G.groups[g - 1].kind == 0 || !G.ext[G.groups[g - 1].res])))) {
+             (!G.ext[G.groups[g - 1].in] && (G.groups[g - 1].kind != 1 || !G.ext[G.groups[g - 1].res])))) {
             Group *grp = &G.groups[g - 1];
             int rc;
             if (grp->kind == 0) {
                 rc = uqk_ib(&grp->desc, G.ptr[grp->in], G.ptr[grp->out], images);
+            } else if (grp->kind == 3) {
+                rc = uqk_uib(&grp->ub, G.ptr[grp->in], G.ptr[grp->out], images);
             } else if (grp->kind == 1) {
                 grp->add.res = G.ptr[grp->res];
                 rc = uqk_conv_add(G.sp + i, G.ptr[grp->in], G.ptr[grp->out], images * G.ts[G.ops[i].a].d[0],
@@ -1204,6 +1320,10 @@ static int enqueue_op(uint32_t i, uint32_t images)
 static int launch_op(uint32_t i, uint32_t images)
 {
     const uint8_t *A = G.arena;
+    if (G.fwd[i] && G.ext[G.ops[i + 1].out]) {
+        G.ptr[G.ops[i].out] = G.ptr[G.ops[i + 1].out];
+        G.ext[G.ops[i].out] = 1;
+    }
     {
         const Op *o = G.ops + i;
         const Tensor *a = G.ts + o->a, *b = G.ts + o->b, *z = G.ts + o->out;
@@ -1227,11 +1347,13 @@ static int launch_op(uint32_t i, uint32_t images)
         }
         case 5:
             /* Every tensor is written once (graph.c:72 forbids redefinition),
-             * so an internal copy can alias its source instead of moving bytes. */
-            if (G.ptr[o->out] == G.act[o->out]) {
+             * so an internal copy can alias its source instead of moving bytes
+             * (in every image slice); a copy into a caller buffer moves them
+             * unless the producer already wrote there (fwd). */
+            if (!G.ext[o->out]) {
                 G.ptr[o->out] = (uint8_t *)G.ptr[o->a];
                 G.ext[o->out] = G.ext[o->a];
-            } else
+            } else if (zp != ap)
                 rc = uqk_d2d(zp, ap, (size_t)images * z->bytes);
             break;
         case 22: rc = uqk_lut(ap, zp, (uint64_t)images * a->bytes, bp, a->type == 3 ? 128u : 0u); break;

@@ -44,10 +44,8 @@
 #include "uqk.h"
 #include "uqk_device.h"
 #include "uqk_internal.h"
+#include "ib_phases.h"
 
-typedef int v16i __attribute__((ext_vector_type(16)));
-
-constexpr int IB_WAVES = 16;
 constexpr int IB_LDS_MAX = 163840;
 
 struct IbArgs {
@@ -78,294 +76,6 @@ struct IbArgs {
     int ks;                    // depthwise kernel size
     int o_e, o_d, o_re, o_rd, o_rp, o_at, o_lut, o_po, o_tw;   // LDS offsets
 };
-
-// Fragments of a wave's weight tile: rows ct*32 + (lane & 31), the 16-byte
-// K slice of each 32-byte step chosen by lane >> 5.
-template <int MAXK>
-__device__ __forceinline__ void ib_load_weights(v4i (&wf)[MAXK], const int8_t *w, int kp, int ks, int ct)
-{
-    const int lane = threadIdx.x & 63;
-    const int8_t *wr = w + (long)(ct * 32 + (lane & 31)) * kp + (lane >> 5) * 16;
-#pragma unroll
-    for (int s = 0; s < MAXK; s++)
-        if (s < ks) wf[s] = *(const v4i *)(wr + s * 32);
-}
-
-// This wave's range of (channel tile, pixel tile) items of a 1x1 phase.
-__device__ __forceinline__ void ib_items(int ctiles, int P, int &i0, int &i1)
-{
-    const int wave = threadIdx.x >> 6, items = ctiles * ((P + 31) >> 5);
-    i0 = wave * items / IB_WAVES;
-    i1 = (wave + 1) * items / IB_WAVES;
-}
-
-// A 1x1 GEMM phase over the image's P pixels: pixel tiles of 32 (MFMA rows,
-// rows of `src` in LDS with stride ss, clamped to P - 1 past the image) by
-// channel tiles of 32 (columns: weights `w`, row stride kp, K = 32 * ks
-// bytes). Each wave takes a contiguous range of (channel tile, pixel tile)
-// items (ib_items), channel tile major, and reloads its weight fragments
-// (wf, of channel tile `loaded`) and its channel's record only when the
-// channel tile changes. `sink(p, c, word)` receives, per lane and for each
-// of its four pixel groups, the requantised bytes of channels c .. c + 3 of
-// pixel p (p < P only).
-template <int MAXK, bool HI, bool CORR, bool LUT, typename Sink>
-__device__ __forceinline__ void ib_gemm(const int8_t *smem, v4i (&wf)[MAXK], int &loaded, const int8_t *w, int kp,
-                                        int ks, const int8_t *src, int ss, int P, int ctiles, int rec_off, int yz,
-                                        int lo, int hi, const int8_t *lut, Sink sink)
-{
-    const int lane = threadIdx.x & 63;
-    const int fr = lane & 31, fh = lane >> 5;
-    const int ptiles = (P + 31) >> 5;
-    int i0, i1;
-    ib_items(ctiles, P, i0, i1);
-    const int vlo = vgpr(lo), vhi = vgpr(hi);
-    Epi e = {};
-    // (channel tile, pixel tile) of the item, stepped along without divisions.
-    int ct = i0 / ptiles, pt = i0 - ct * ptiles;
-    for (int item = i0; item < i1; item++, pt = pt + 1 < ptiles ? pt + 1 : 0, ct += pt == 0) {
-        if (ct != loaded) {
-            ib_load_weights<MAXK>(wf, w, kp, ks, ct);
-            loaded = ct;
-        }
-        e = load_epi((const int4 *)(smem + rec_off), ct * 32 + fr);
-        const int8_t *sr = src + __mul24(min(pt * 32 + fr, P - 1), ss) + fh * 16;
-        v16i acc;
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[r] = 0;
-#pragma unroll
-        for (int s = 0; s < MAXK; s++)
-            if (s < ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i *)(sr + s * 32), wf[s], acc, 0, 0, 0);
-        // acc[4g + i]: pixel pt*32 + 8g + 4fh + i, channel ct*32 + fr.
-        const int c = ct * 32 + (fr & ~3);
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            int v[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                v[i] = conv_requant<HI, CORR>(acc[4 * g + i], e, yz, vlo, vhi);
-                if (LUT) v[i] = lut[v[i] + 128];
-            }
-            const int word = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
-            const int p = pt * 32 + 8 * g + 4 * fh + (lane & 3);
-            if (p < P) sink(p, c, word);
-        }
-    }
-}
-
-// ib_gemm with the requantisation variant (a wave-uniform mode) and the
-// presence of a post table as template arguments.
-template <int MAXK, typename Sink>
-__device__ __forceinline__ void ib_gemm_mode(int mode, const int8_t *smem, v4i (&wf)[MAXK], int &loaded,
-                                             const int8_t *w, int kp, int ks, const int8_t *src, int ss, int P,
-                                             int ctiles, int rec_off, int yz, int lo, int hi, const int8_t *lut,
-                                             Sink sink)
-{
-#define IB_GEMM(H, C, L) \
-    ib_gemm<MAXK, H, C, L>(smem, wf, loaded, w, kp, ks, src, ss, P, ctiles, rec_off, yz, lo, hi, lut, sink)
-    switch (mode * 2 + (lut != nullptr)) {
-    case 0: IB_GEMM(false, false, false); break;
-    case 1: IB_GEMM(false, false, true); break;
-    case 2: IB_GEMM(true, false, false); break;
-    case 3: IB_GEMM(true, false, true); break;
-    case 4: IB_GEMM(false, true, false); break;
-    case 5: IB_GEMM(false, true, true); break;
-    case 6: IB_GEMM(true, true, false); break;
-    default: IB_GEMM(true, true, true); break;
-    }
-#undef IB_GEMM
-}
-
-// The project phase's GEMM, in 16x16 tiles on v_mfma_i32_16x16x64_i8 (finer
-// items than 32x32 tiles: a 7x7 map has only two 32-pixel tiles): pixel
-// tiles of 16 (rows of `src`, stride ss) by channel tiles of 16 (weights
-// `w`, row stride kp, zero past the K bytes, so that the source bytes a K
-// tail reads past its rows add nothing), K = 64 * ks bytes. Items as in
-// ib_gemm. `sink(p, c, word)`: channels c .. c + 3 of pixel p.
-template <int MAXK, bool HI, bool CORR, bool LUT, typename Sink>
-__device__ __forceinline__ void ib_gemm16(const int8_t *smem, const int8_t *w, int kp, int ks, const int8_t *src,
-                                          int ss, int P, int ctiles, int rec_off, int yz, int lo, int hi,
-                                          const int8_t *lut, Sink sink)
-{
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int lr = lane & 15, lg = lane >> 4;
-    const int ptiles = (P + 15) >> 4, items = ctiles * ptiles;
-    const int i0 = wave * items / IB_WAVES, i1 = (wave + 1) * items / IB_WAVES;
-    const int vlo = vgpr(lo), vhi = vgpr(hi);
-    v4i wf[MAXK];
-    Epi e = {};
-    int loaded = -1;
-    int ct = i0 / ptiles, pt = i0 - ct * ptiles;
-    for (int item = i0; item < i1; item++, pt = pt + 1 < ptiles ? pt + 1 : 0, ct += pt == 0) {
-        if (ct != loaded) {
-            const int8_t *wr = w + (long)(ct * 16 + lr) * kp + lg * 16;
-#pragma unroll
-            for (int s = 0; s < MAXK; s++)
-                if (s < ks) wf[s] = *(const v4i *)(wr + s * 64);
-            e = load_epi((const int4 *)(smem + rec_off), ct * 16 + lr);
-            loaded = ct;
-        }
-        const int8_t *sr = src + __mul24(min(pt * 16 + lr, P - 1), ss) + lg * 16;
-        v4i acc = {0, 0, 0, 0};
-#pragma unroll
-        for (int s = 0; s < MAXK; s++)
-            if (s < ks) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(const v4i *)(sr + s * 64), wf[s], acc, 0, 0, 0);
-        // acc[i]: pixel pt*16 + 4*lg + i, channel ct*16 + lr.
-        int v[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            v[i] = conv_requant<HI, CORR>(acc[i], e, yz, vlo, vhi);
-            if (LUT) v[i] = lut[v[i] + 128];
-        }
-        const int word = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
-        const int p = pt * 16 + lg * 4 + (lane & 3);
-        if (p < P) sink(p, ct * 16 + (lr & ~3), word);
-    }
-}
-
-template <int MAXK, typename Sink>
-__device__ __forceinline__ void ib_gemm16_mode(int mode, const int8_t *smem, const int8_t *w, int kp, int ks,
-                                               const int8_t *src, int ss, int P, int ctiles, int rec_off, int yz,
-                                               int lo, int hi, const int8_t *lut, Sink sink)
-{
-#define IB_GEMM(H, C, L) ib_gemm16<MAXK, H, C, L>(smem, w, kp, ks, src, ss, P, ctiles, rec_off, yz, lo, hi, lut, sink)
-    switch (mode * 2 + (lut != nullptr)) {
-    case 0: IB_GEMM(false, false, false); break;
-    case 1: IB_GEMM(false, false, true); break;
-    case 2: IB_GEMM(true, false, false); break;
-    case 3: IB_GEMM(true, false, true); break;
-    case 4: IB_GEMM(false, true, false); break;
-    case 5: IB_GEMM(false, true, true); break;
-    case 6: IB_GEMM(true, true, false); break;
-    default: IB_GEMM(true, true, true); break;
-    }
-#undef IB_GEMM
-}
-
-// Depthwise phase: items (16-channel group, 16-pixel tile), group major, a
-// contiguous range per wave; the block-diagonal tap operands (from the tap
-// words staged in LDS) and the channel's record are rebuilt when the group
-// changes.
-template <int KS, bool HI, bool CORR, bool LUT>
-__device__ __forceinline__ void ib_dw(const IbArgs &a, const int8_t *smem, const int8_t *E, int8_t *D,
-                                      const int8_t *lut_s, const int *padoff, const int *tw, int plane)
-{
-    constexpr int T = KS * KS, NG = (T + 3) / 4, NWK = KS > 4 ? 2 : 1;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int lr = lane & 15, lg = lane >> 4;
-    const int tiles = (a.P + 15) >> 4, items = (a.Ce >> 4) * tiles;
-    const int i0 = wave * items / IB_WAVES, i1 = (wave + 1) * items / IB_WAVES;
-    const int vlo = vgpr(a.d_lo), vhi = vgpr(a.d_hi);
-    const int corner = a.pt * a.cols_p + a.pl;
-    int off[NG];
-#pragma unroll
-    for (int m = 0; m < NG; m++) {
-        const int t = 4 * m + lg, ky = t / KS, kx = t - ky * KS;
-        off[m] = t < T ? (ky * a.cols_p + kx) * 16 : 0;
-    }
-    v4i B[NG];
-    Epi e = {};
-    int loaded = -1;
-    // (group, tile) of the item, stepped along without divisions; gplane is
-    // the group's window plane less the window corner.
-    int g = i0 / tiles, t16 = i0 - g * tiles;
-    const int8_t *gplane = E;
-    for (int item = i0; item < i1; item++, t16 = t16 + 1 < tiles ? t16 + 1 : 0, g += t16 == 0) {
-        if (g != loaded) {
-            gplane = E + (g * plane - corner) * 16;
-#pragma unroll
-            for (int m = 0; m < NG; m++) {
-                const int t = 4 * m + lg, ky = t / KS, kx = t - ky * KS;
-                int wb = 0;
-                if (t < T) wb = (tw[(ky * NWK + (kx >> 2)) * a.Ce + g * 16 + lr] >> (8 * (kx & 3))) & 0xff;
-                const int word = wb << (8 * (lr & 3)), q = lr >> 2;
-                B[m] = (v4i){q == 0 ? word : 0, q == 1 ? word : 0, q == 2 ? word : 0, q == 3 ? word : 0};
-            }
-            e = load_epi((const int4 *)(smem + a.o_rd), g * 16 + lr);
-            loaded = g;
-        }
-        // The window corner of pixel p is its padded position less (pt, pl).
-        const int p = min(t16 * 16 + lr, a.P - 1);
-        const int8_t *base = gplane + padoff[p] * 16;
-        v4i acc = {0, 0, 0, 0};
-#pragma unroll
-        for (int m = 0; m < NG; m++)
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(const v4i *)(base + off[m]), B[m], acc, 0, 0, 0);
-        // acc[i]: pixel t16*16 + 4*lg + i, channel g*16 + lr.
-        int v[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            v[i] = conv_requant<HI, CORR>(acc[i], e, a.d_yz, vlo, vhi);
-            if (LUT) v[i] = lut_s[256 + v[i] + 128];
-        }
-        const int word = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
-        const int px = t16 * 16 + lg * 4 + (lane & 3);
-        if (px < a.P) *(int *)(D + __mul24(px, a.ds) + g * 16 + (lr & ~3)) = word;
-    }
-}
-
-// The 3x3 depthwise on 32x32 tiles (v_mfma_i32_32x32x32_i8, one per tap):
-// 32 pixels (rows: 16-byte reads of the window planes of the tile's two
-// 16-channel groups) by 32 channels (columns: block-diagonal, lane (channel
-// n, half h) holds w[tap][n] in byte n % 16 of the half that contains n).
-// A lane's 16 results share one channel, so one record per lane, and the
-// epilogue is the expand's: 4x4 byte transposes into 4-byte writes of D.
-// Items (32-channel tile, 32-pixel tile), channel tile major; the taps'
-// operands and the record are rebuilt when the channel tile changes.
-template <bool HI, bool CORR, bool LUT>
-__device__ __forceinline__ void ib_dw3_32(const IbArgs &a, const int8_t *smem, const int8_t *E, int8_t *D,
-                                          const int8_t *lut_s, const int *padoff, const int *tw, int plane)
-{
-    const int lane = threadIdx.x & 63;
-    const int fr = lane & 31, fh = lane >> 5;
-    const int ptiles = (a.P + 31) >> 5;
-    int i0, i1;
-    ib_items(a.Ce >> 5, a.P, i0, i1);
-    const int vlo = vgpr(a.d_lo), vhi = vgpr(a.d_hi);
-    const int corner = a.pt * a.cols_p + a.pl;
-    int off[9];
-#pragma unroll
-    for (int t = 0; t < 9; t++) off[t] = ((t / 3) * a.cols_p + t % 3) * 16;
-    v4i B[9];
-    Epi e = {};
-    int loaded = -1;
-    const int8_t *gplane = E;
-    int ct = i0 / ptiles, pt = i0 - ct * ptiles;
-    for (int item = i0; item < i1; item++, pt = pt + 1 < ptiles ? pt + 1 : 0, ct += pt == 0) {
-        if (ct != loaded) {
-            const int c = ct * 32 + fr, q = (fr & 15) >> 2;
-            const bool mine = (fr >> 4) == fh;
-#pragma unroll
-            for (int t = 0; t < 9; t++) {
-                const int wb = mine ? (tw[(t / 3) * a.Ce + c] >> (8 * (t % 3))) & 0xff : 0;
-                const int word = wb << (8 * (fr & 3));
-                B[t] = (v4i){q == 0 ? word : 0, q == 1 ? word : 0, q == 2 ? word : 0, q == 3 ? word : 0};
-            }
-            e = load_epi((const int4 *)(smem + a.o_rd), c);
-            gplane = E + ((ct * 2 + fh) * plane - corner) * 16;
-            loaded = ct;
-        }
-        const int8_t *base = gplane + padoff[min(pt * 32 + fr, a.P - 1)] * 16;
-        v16i acc;
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[r] = 0;
-#pragma unroll
-        for (int t = 0; t < 9; t++) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i *)(base + off[t]), B[t], acc, 0, 0, 0);
-        // acc[4g + i]: pixel pt*32 + 8g + 4fh + i, channel ct*32 + fr.
-        const int c = ct * 32 + (fr & ~3);
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            int v[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                v[i] = conv_requant<HI, CORR>(acc[4 * g + i], e, a.d_yz, vlo, vhi);
-                if (LUT) v[i] = lut_s[256 + v[i] + 128];
-            }
-            const int word = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
-            const int px = pt * 32 + 8 * g + 4 * fh + (lane & 3);
-            if (px < a.P) *(int *)(D + __mul24(px, a.ds) + c) = word;
-        }
-    }
-}
 
 template <int KS>
 __global__ __launch_bounds__(64 * IB_WAVES) void k_ib(IbArgs a)
@@ -423,22 +133,11 @@ __global__ __launch_bounds__(64 * IB_WAVES) void k_ib(IbArgs a)
     __syncthreads();
 
     // Phase 2: depthwise into D.
-#define IB_DW(H, C, L)                                                   \
-    do {                                                                 \
-        if (KS == 3) ib_dw3_32<H, C, L>(a, smem, E, D, lut_s, padoff, tw, plane); \
-        else ib_dw<KS, H, C, L>(a, smem, E, D, lut_s, padoff, tw, plane); \
-    } while (0)
-    switch (a.d_mode * 2 + (a.lut_d != nullptr)) {
-    case 0: IB_DW(false, false, false); break;
-    case 1: IB_DW(false, false, true); break;
-    case 2: IB_DW(true, false, false); break;
-    case 3: IB_DW(true, false, true); break;
-    case 4: IB_DW(false, true, false); break;
-    case 5: IB_DW(false, true, true); break;
-    case 6: IB_DW(true, true, false); break;
-    default: IB_DW(true, true, true); break;
+    {
+        const DwPh g = {a.P, a.Ce, a.ds, a.cols_p, a.pt * a.cols_p + a.pl, a.d_yz, a.d_lo, a.d_hi,
+                        (const int4 *)(smem + a.o_rd), a.lut_d ? lut_s + 256 : nullptr};
+        ib_dw_mode<KS>(a.d_mode, g, E, D, padoff, tw, plane);
     }
-#undef IB_DW
     __syncthreads();
 
     // Phase 3: project (+ residual add) into the output stage over E, then
@@ -473,8 +172,12 @@ __global__ __launch_bounds__(64 * IB_WAVES) void k_ib(IbArgs a)
         }
         *(int *)(S + __mul24(p, a.Cout) + c) = word;
     };
-    // 32x32 tiles when every wave gets one, else 16x16 tiles.
-    if ((a.Cout >> 5) * ((a.P + 31) >> 5) >= IB_WAVES) {
+    // 32x32 tiles when they leave the busiest wave no more results per lane
+    // than 16x16 tiles (16 per 32x32 item, 4 per 16x16 item), else 16x16:
+    // on 14x14x96 outputs 21 items of 32x32 (two for some waves, 32 results)
+    // against 78 of 16x16 (at most five, 20 results).
+    const int i32 = (a.Cout >> 5) * ((a.P + 31) >> 5), i16 = (a.Cout >> 4) * ((a.P + 15) >> 4);
+    if ((i32 + IB_WAVES - 1) / IB_WAVES * 16 <= (i16 + IB_WAVES - 1) / IB_WAVES * 4) {
         v4i wfp[16];
         int wfp_ct = -1;
         ib_gemm_mode<16>(a.p_mode, smem, wfp, wfp_ct, a.wp, a.kpp, a.Ce >> 5, D, a.ds, a.P, a.Cout >> 5, a.o_rp,

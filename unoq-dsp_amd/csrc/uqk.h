@@ -80,6 +80,36 @@ typedef struct {
 size_t uqk_ib_lds(int P, int H, int W, int Cin, int Ce, int Cout, int ks, size_t *offsets);
 int uqk_ib(const UQKIb *f, const void *x, void *y, uint32_t images);
 
+/* Banded universal inverted bottleneck (uib.hip): [start depthwise, stride
+ * 1] -> 1x1 expand -> [depthwise, stride 1 or 2] -> 1x1 project [-> residual
+ * add with the block input], one workgroup per image and band of R output
+ * rows. k0 / k: the depthwise kernel sizes (3 or 5; 0: absent, not both).
+ * Tap words are the window form's [ky][k > 4 ? 2 : 1][C]. */
+typedef struct {
+    int32_t H, W, Ho, Wo, Cin, Ce, Cout;
+    int32_t k0, p0t, p0l;
+    const void *dw0, *epi0, *lut0;
+    int32_t m0, yz0, lo0, hi0, xz0;
+    const void *we, *epi_e, *lut_e;
+    int32_t kpe, e_mode, e_yz, e_lo, e_hi;
+    int32_t k, s, pt, pl;
+    const void *dww, *epi_d, *lut_d;
+    int32_t d_mode, d_yz, d_lo, d_hi, d_xz;
+    const void *wp, *epi_p, *lut_p;
+    int32_t kpp, p_mode, p_yz, p_lo, p_hi;
+    int32_t has_add, add_x_first;
+    const void *add_tab;
+    int32_t a_m, a_s, a_yz, a_lo, a_hi;
+    int32_t R;                 /* output rows per band: set by uqk_uib_plan */
+} UQKUib;
+
+/* Sets f->R to the most output rows per band whose workgroup fits in LDS and
+ * returns that LDS size; 0 (and R = 0) when the block does not fit the
+ * kernel (channel counts multiples of 32, Cin <= 256, Ce <= 512, pads within
+ * the kernels, an add only at stride 1 with Cin == Cout). */
+size_t uqk_uib_plan(UQKUib *f);
+int uqk_uib(const UQKUib *f, const void *x, void *y, uint32_t images);
+
 /* Stem conv fused with the 3x3 stride-2 conv over its 32-channel output
  * (stem.hip): whether the pair fits, and its launch (images of the stem's
  * input to the 3x3's output). */

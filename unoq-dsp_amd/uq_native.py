@@ -67,7 +67,7 @@ def open_library(path=None):
         fn.argtypes = args
     # Test hooks outside the plan ABI: launches of the large-tile GEMM, of the
     # fused bottleneck kernel and of the fused stem kernel.
-    for hook in ("uqk_gemm_launches", "uqk_ib_launches", "uqk_stem_conv_launches"):
+    for hook in ("uqk_gemm_launches", "uqk_ib_launches", "uqk_stem_conv_launches", "uqk_uib_launches"):
         getattr(lib, hook).restype = C.c_uint64
         getattr(lib, hook).argtypes = []
     return lib
