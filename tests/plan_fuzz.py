@@ -498,11 +498,12 @@ def ib_plan(seed):
     return p.build(z)
 
 
-def uib_lds(H, W, Ho, Wo, cin, ce, cout, k0, k, s, add, R):
+def uib_lds(H, W, Ho, Wo, cin, ce, cout, k0, k, s, add, R, rec_lds=1):
     """LDS bytes of the banded bottleneck kernel's workgroup for bands of R
     output rows (its layout: staged input, start-depthwise rows, window
-    planes, depthwise rows, records, tables, position tables, tap words), 0
-    when over 160 KiB or when the output stage does not fit."""
+    planes, depthwise rows, records, tables, position tables, tap words;
+    rec_lds: the expand and depthwise records in LDS too), 0 when over 160
+    KiB or when the output stage does not fit."""
     def up(v):
         return (v + 15) & ~15
     re = (R - 1) * s + k if k else R
@@ -516,7 +517,8 @@ def uib_lds(H, W, Ho, Wo, cin, ce, cout, k0, k, s, add, R):
     o += up((ce // 16) * re * cols_p * 16 if k else 0)
     d = o
     o += up((po if k else pe) * (ce + 16)) + 64
-    o += (cin * 32 if k0 else 0) + ce * 32 + (ce * 32 if k else 0) + cout * 32 + (2048 if add else 0) + 1024
+    o += (cin * 32 if k0 else 0) + (ce * 32 if rec_lds else 0) + (ce * 32 if k and rec_lds else 0) + cout * 32
+    o += (2048 if add else 0) + 1024
     o += up(pe * 4 if k0 else 0) + up(pe * 4 if k else 0) + up(po * 4 if k else 0) + up(po * 4 if add else 0)
     o += up(k0 * (2 if k0 > 4 else 1) * cin * 4) + up(k * (2 if k > 4 else 1) * ce * 4)
     if po * cout > ((d - e) if k else (e - x1)):
@@ -549,12 +551,14 @@ def dw_window_form(c, oh, ow, k, s):
 
 
 def uib_rows(H, W, Ho, Wo, cin, ce, cout, k0, k, s, add):
-    """Output rows per band the banded bottleneck kernel takes: the most
-    whose workgroup fits (0: none does)."""
+    """(R, rec_lds): the output rows per band the banded bottleneck kernel
+    takes, the most whose workgroup fits, with the expand and depthwise
+    records in LDS when they fit too ((0, 0): nothing fits)."""
     for R in range(Ho, 0, -1):
-        if uib_lds(H, W, Ho, Wo, cin, ce, cout, k0, k, s, add, R):
-            return R
-    return 0
+        for rec_lds in (1, 0):
+            if uib_lds(H, W, Ho, Wo, cin, ce, cout, k0, k, s, add, R, rec_lds):
+                return R, rec_lds
+    return 0, 0
 
 
 def uib_plan(seed):
@@ -607,7 +611,7 @@ def uib_block(seed):
             ho, wo = h, w
         if (k0 and not dw_window_form(cin, h, w, k0, 1)) or (k and not dw_window_form(ce, ho, wo, k, s)):
             continue
-        rows = uib_rows(h, w, ho, wo, cin, ce, cout, k0, k, s, add)
+        rows = uib_rows(h, w, ho, wo, cin, ce, cout, k0, k, s, add)[0]
         if rows:
             break
     x = p.input((1, h, w, cin), zp=int(rng.integers(1, -128, 127)[0]))

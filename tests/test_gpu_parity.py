@@ -338,12 +338,12 @@ def test_banded_bottleneck_plans(lib, monkeypatch, seed):
     assert lib.uqk_uib_launches() == before
 
 
-@pytest.mark.parametrize("mode,launches", [("1", 1), ("2", 3)])
+@pytest.mark.parametrize("mode,launches", [("1", 2), ("2", 3)])
 def test_mnv4_banded_groups(lib, monkeypatch, mode, launches):
-    """MobileNetV4's 14x14 ExtraDW block runs on the banded kernel in one
-    band by default; with UQ_FUSE_UIB=2 its 28x28 block with a stride-2
-    depthwise (five bands) and its 7x7 ExtraDW block (two bands) do too; the
-    bytes match the oracle either way (batch 3, one image slice)."""
+    """MobileNetV4's 14x14 and 7x7 ExtraDW blocks run on the banded kernel in
+    one band by default (the 7x7 one with its records read from L2); with
+    UQ_FUSE_UIB=2 its 28x28 block with a stride-2 depthwise (five bands) does
+    too; the bytes match the oracle either way (batch 3, one image slice)."""
     monkeypatch.setenv("UQ_FUSE_UIB", mode)
     plan, _ = W.mnv4()
     x = P.random_input(plan, 3, 77)

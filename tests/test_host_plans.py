@@ -24,20 +24,20 @@ class UQKUib(C.Structure):
                 + [(n, _P) for n in "wp epi_p lut_p".split()]
                 + [(n, _I) for n in "kpp p_mode p_yz p_lo p_hi has_add add_x_first".split()]
                 + [("add_tab", _P)]
-                + [(n, _I) for n in "a_m a_s a_yz a_lo a_hi R".split()])
+                + [(n, _I) for n in "a_m a_s a_yz a_lo a_hi R rec_lds".split()])
 
 
 def _plan(lib, **kw):
     u = UQKUib(**kw)
     lds = lib.uqk_uib_plan(C.byref(u))
-    return lds, u.R
+    return lds, u.R, u.rec_lds
 
 
 def test_uib_plan_matches_layout():
     lib = open_library()
     lib.uqk_uib_plan.restype = C.c_size_t
     rng = np.random.default_rng(5)
-    checked = fused = 0
+    checked = fused = global_records = 0
     for _ in range(3000):
         k0 = int(rng.choice([0, 3, 5]))
         k = int(rng.choice([3, 5])) if k0 == 0 else int(rng.choice([0, 3, 5]))
@@ -50,14 +50,15 @@ def test_uib_plan_matches_layout():
         if Ho < 1 or Wo < 1:
             continue
         add = int(s == 1 and cin == cout and rng.integers(0, 2) == 1)
-        lds, R = _plan(lib, H=H, W=W, Ho=Ho, Wo=Wo, Cin=cin, Ce=ce, Cout=cout, k0=k0, p0t=p0t, p0l=p0l, k=k, s=s,
-                       pt=pt, pl=pl, has_add=add)
+        lds, R, rec_lds = _plan(lib, H=H, W=W, Ho=Ho, Wo=Wo, Cin=cin, Ce=ce, Cout=cout, k0=k0, p0t=p0t, p0l=p0l,
+                                k=k, s=s, pt=pt, pl=pl, has_add=add)
         want = uib_rows(H, W, Ho, Wo, cin, ce, cout, k0, k, s, add)
-        assert R == want, (H, W, cin, ce, cout, k0, k, s, add)
-        assert lds == (uib_lds(H, W, Ho, Wo, cin, ce, cout, k0, k, s, add, R) if R else 0)
+        assert (R, rec_lds) == want, (H, W, cin, ce, cout, k0, k, s, add)
+        assert lds == (uib_lds(H, W, Ho, Wo, cin, ce, cout, k0, k, s, add, R, rec_lds) if R else 0)
         checked += 1
         fused += R > 0
-    assert checked > 2000 and 0 < fused < checked
+        global_records += R > 0 and not rec_lds
+    assert checked > 2000 and 0 < fused < checked and global_records > 0
 
 
 def test_uib_plan_refuses_outside_shapes():
@@ -65,12 +66,16 @@ def test_uib_plan_refuses_outside_shapes():
     lib.uqk_uib_plan.restype = C.c_size_t
     base = dict(H=14, W=14, Ho=14, Wo=14, Cin=96, Ce=384, Cout=96, k0=3, p0t=1, p0l=1, k=0, s=1, has_add=1)
     assert _plan(lib, **base)[0] > 0
+    # MobileNetV4's 7x7 ExtraDW block (5x5 start and middle depthwise, 128 ->
+    # 512 -> 128 with the add) fits one band with its records read from L2.
+    assert _plan(lib, H=7, W=7, Ho=7, Wo=7, Cin=128, Ce=512, Cout=128, k0=5, p0t=2, p0l=2, k=5, s=1, pt=2, pl=2,
+                 has_add=1)[1:] == (7, 0)
     for change in (dict(k0=0),                       # neither depthwise
                    dict(Cin=80), dict(Ce=528), dict(Cout=48),   # channel counts
                    dict(Ce=544),                     # Ce > 512
                    dict(k0=7), dict(p0t=3),          # start depthwise kernel and pads
                    dict(Cout=64),                    # an add needs Cin == Cout
                    dict(Ho=7, Wo=7)):                # without a depthwise the map keeps its size
-        assert _plan(lib, **dict(base, **change)) == (0, 0), change
+        assert _plan(lib, **dict(base, **change))[:2] == (0, 0), change
     # An add after a stride-2 depthwise is refused.
-    assert _plan(lib, **dict(base, k=3, s=2, pt=0, pl=0, Ho=7, Wo=7, Cout=96)) == (0, 0)
+    assert _plan(lib, **dict(base, k=3, s=2, pt=0, pl=0, Ho=7, Wo=7, Cout=96))[:2] == (0, 0)

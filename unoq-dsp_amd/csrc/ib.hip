@@ -126,8 +126,9 @@ __global__ __launch_bounds__(64 * IB_WAVES) void k_ib(IbArgs a)
     // Phase 1: expand into the window planes.
     v4i wfe[8];
     int wfe_ct = -1;
-    ib_gemm_mode<8>(a.e_mode, smem, wfe, wfe_ct, a.we, a.kpe, a.Cin >> 5, X, a.xs, a.P, a.Ce >> 5, a.o_re, a.e_yz,
-                    a.e_lo, a.e_hi, a.lut_e ? lut_s : nullptr, [&](int p, int c, int word) {
+    ib_gemm_mode<8>(a.e_mode, wfe, wfe_ct, a.we, a.kpe, a.Cin >> 5, X, a.xs, a.P, a.Ce >> 5,
+                    (const int4 *)(smem + a.o_re), a.e_yz, a.e_lo, a.e_hi, a.lut_e ? lut_s : nullptr,
+                    [&](int p, int c, int word) {
                         *(int *)(E + (__mul24(c >> 4, plane) + padoff[p]) * 16 + (c & 15)) = word;
                     });
     __syncthreads();
@@ -180,11 +181,13 @@ __global__ __launch_bounds__(64 * IB_WAVES) void k_ib(IbArgs a)
     if ((i32 + IB_WAVES - 1) / IB_WAVES * 16 <= (i16 + IB_WAVES - 1) / IB_WAVES * 4) {
         v4i wfp[16];
         int wfp_ct = -1;
-        ib_gemm_mode<16>(a.p_mode, smem, wfp, wfp_ct, a.wp, a.kpp, a.Ce >> 5, D, a.ds, a.P, a.Cout >> 5, a.o_rp,
-                         a.p_yz, a.p_lo, a.p_hi, a.lut_p ? lut_s + 512 : nullptr, project_sink);
+        ib_gemm_mode<16>(a.p_mode, wfp, wfp_ct, a.wp, a.kpp, a.Ce >> 5, D, a.ds, a.P, a.Cout >> 5,
+                         (const int4 *)(smem + a.o_rp), a.p_yz, a.p_lo, a.p_hi, a.lut_p ? lut_s + 512 : nullptr,
+                         project_sink);
     } else {
-        ib_gemm16_mode<8>(a.p_mode, smem, a.wp, a.kpp, (a.Ce + 63) >> 6, D, a.ds, a.P, a.Cout >> 4, a.o_rp, a.p_yz,
-                          a.p_lo, a.p_hi, a.lut_p ? lut_s + 512 : nullptr, project_sink);
+        ib_gemm16_mode<8>(a.p_mode, a.wp, a.kpp, (a.Ce + 63) >> 6, D, a.ds, a.P, a.Cout >> 4,
+                          (const int4 *)(smem + a.o_rp), a.p_yz, a.p_lo, a.p_hi, a.lut_p ? lut_s + 512 : nullptr,
+                          project_sink);
     }
     __syncthreads();
     int8_t *yim = a.y + n * a.P * a.Cout;

@@ -39,13 +39,13 @@ __device__ __forceinline__ void ib_items(int ctiles, int P, int &i0, int &i1)
 // channel tiles of 32 (columns: weights `w`, row stride kp, K = 32 * ks
 // bytes). Each wave takes a contiguous range of (channel tile, pixel tile)
 // items (ib_items), channel tile major, and reloads its weight fragments
-// (wf, of channel tile `loaded`) and its channel's record only when the
-// channel tile changes. `sink(p, c, word)` receives, per lane and for each
+// (wf, of channel tile `loaded`) and its channel's record (from `rec`, in
+// LDS or global memory) only when the channel tile changes. `sink(p, c, word)` receives, per lane and for each
 // of its four pixel groups, the requantised bytes of channels c .. c + 3 of
 // pixel p (p < P only).
 template <int MAXK, bool HI, bool CORR, bool LUT, typename Sink>
-__device__ __forceinline__ void ib_gemm(const int8_t *smem, v4i (&wf)[MAXK], int &loaded, const int8_t *w, int kp,
-                                        int ks, const int8_t *src, int ss, int P, int ctiles, int rec_off, int yz,
+__device__ __forceinline__ void ib_gemm(v4i (&wf)[MAXK], int &loaded, const int8_t *w, int kp, int ks,
+                                        const int8_t *src, int ss, int P, int ctiles, const int4 *rec, int yz,
                                         int lo, int hi, const int8_t *lut, Sink sink)
 {
     const int lane = threadIdx.x & 63;
@@ -55,6 +55,7 @@ __device__ __forceinline__ void ib_gemm(const int8_t *smem, v4i (&wf)[MAXK], int
     ib_items(ctiles, P, i0, i1);
     const int vlo = vgpr(lo), vhi = vgpr(hi);
     Epi e = {};
+    int have = -1;
     // (channel tile, pixel tile) of the item, stepped along without divisions.
     int ct = i0 / ptiles, pt = i0 - ct * ptiles;
     for (int item = i0; item < i1; item++, pt = pt + 1 < ptiles ? pt + 1 : 0, ct += pt == 0) {
@@ -62,7 +63,10 @@ __device__ __forceinline__ void ib_gemm(const int8_t *smem, v4i (&wf)[MAXK], int
             ib_load_weights<MAXK>(wf, w, kp, ks, ct);
             loaded = ct;
         }
-        e = load_epi((const int4 *)(smem + rec_off), ct * 32 + fr);
+        if (ct != have) {
+            e = load_epi(rec, ct * 32 + fr);
+            have = ct;
+        }
         const int8_t *sr = src + __mul24(min(pt * 32 + fr, P - 1), ss) + fh * 16;
         v16i acc;
 #pragma unroll
@@ -90,13 +94,11 @@ __device__ __forceinline__ void ib_gemm(const int8_t *smem, v4i (&wf)[MAXK], int
 // ib_gemm with the requantisation variant (a wave-uniform mode) and the
 // presence of a post table as template arguments.
 template <int MAXK, typename Sink>
-__device__ __forceinline__ void ib_gemm_mode(int mode, const int8_t *smem, v4i (&wf)[MAXK], int &loaded,
-                                             const int8_t *w, int kp, int ks, const int8_t *src, int ss, int P,
-                                             int ctiles, int rec_off, int yz, int lo, int hi, const int8_t *lut,
-                                             Sink sink)
+__device__ __forceinline__ void ib_gemm_mode(int mode, v4i (&wf)[MAXK], int &loaded, const int8_t *w, int kp,
+                                             int ks, const int8_t *src, int ss, int P, int ctiles, const int4 *rec,
+                                             int yz, int lo, int hi, const int8_t *lut, Sink sink)
 {
-#define IB_GEMM(H, C, L) \
-    ib_gemm<MAXK, H, C, L>(smem, wf, loaded, w, kp, ks, src, ss, P, ctiles, rec_off, yz, lo, hi, lut, sink)
+#define IB_GEMM(H, C, L) ib_gemm<MAXK, H, C, L>(wf, loaded, w, kp, ks, src, ss, P, ctiles, rec, yz, lo, hi, lut, sink)
     switch (mode * 2 + (lut != nullptr)) {
     case 0: IB_GEMM(false, false, false); break;
     case 1: IB_GEMM(false, false, true); break;
@@ -117,9 +119,9 @@ __device__ __forceinline__ void ib_gemm_mode(int mode, const int8_t *smem, v4i (
 // tail reads past its rows add nothing), K = 64 * ks bytes. Items as in
 // ib_gemm. `sink(p, c, word)`: channels c .. c + 3 of pixel p.
 template <int MAXK, bool HI, bool CORR, bool LUT, typename Sink>
-__device__ __forceinline__ void ib_gemm16(const int8_t *smem, const int8_t *w, int kp, int ks, const int8_t *src,
-                                          int ss, int P, int ctiles, int rec_off, int yz, int lo, int hi,
-                                          const int8_t *lut, Sink sink)
+__device__ __forceinline__ void ib_gemm16(const int8_t *w, int kp, int ks, const int8_t *src, int ss, int P,
+                                          int ctiles, const int4 *rec, int yz, int lo, int hi, const int8_t *lut,
+                                          Sink sink)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;
@@ -136,7 +138,7 @@ __device__ __forceinline__ void ib_gemm16(const int8_t *smem, const int8_t *w, i
 #pragma unroll
             for (int s = 0; s < MAXK; s++)
                 if (s < ks) wf[s] = *(const v4i *)(wr + s * 64);
-            e = load_epi((const int4 *)(smem + rec_off), ct * 16 + lr);
+            e = load_epi(rec, ct * 16 + lr);
             loaded = ct;
         }
         const int8_t *sr = src + __mul24(min(pt * 16 + lr, P - 1), ss) + lg * 16;
@@ -158,11 +160,11 @@ __device__ __forceinline__ void ib_gemm16(const int8_t *smem, const int8_t *w, i
 }
 
 template <int MAXK, typename Sink>
-__device__ __forceinline__ void ib_gemm16_mode(int mode, const int8_t *smem, const int8_t *w, int kp, int ks,
-                                               const int8_t *src, int ss, int P, int ctiles, int rec_off, int yz,
-                                               int lo, int hi, const int8_t *lut, Sink sink)
+__device__ __forceinline__ void ib_gemm16_mode(int mode, const int8_t *w, int kp, int ks, const int8_t *src, int ss,
+                                               int P, int ctiles, const int4 *rec, int yz, int lo, int hi,
+                                               const int8_t *lut, Sink sink)
 {
-#define IB_GEMM(H, C, L) ib_gemm16<MAXK, H, C, L>(smem, w, kp, ks, src, ss, P, ctiles, rec_off, yz, lo, hi, lut, sink)
+#define IB_GEMM(H, C, L) ib_gemm16<MAXK, H, C, L>(w, kp, ks, src, ss, P, ctiles, rec, yz, lo, hi, lut, sink)
     switch (mode * 2 + (lut != nullptr)) {
     case 0: IB_GEMM(false, false, false); break;
     case 1: IB_GEMM(false, false, true); break;
@@ -297,7 +299,8 @@ __device__ __forceinline__ void ib_dw3_32(const DwPh &a, const int8_t *E, int8_t
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[r] = 0;
 #pragma unroll
-        for (int t = 0; t < 9; t++) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i *)(base + off[t]), B[t], acc, 0, 0, 0);
+        for (int t = 0; t < 9; t++)
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i *)(base + off[t]), B[t], acc, 0, 0, 0);
         // acc[4g + i]: pixel pt*32 + 8g + 4fh + i, channel ct*32 + fr.
         const int c = ct * 32 + (fr & ~3);
 #pragma unroll

@@ -72,6 +72,7 @@ struct UibArgs {
     int a_hs;
     unsigned m_w, m_wo, m_cq, m_c0;   // udiv_magic(W), (Wo), (Cin / 16), (cols0)
     int xs, x1s, ds;           // LDS row strides: X rows, X1 rows, D rows
+    int rec_lds;               // expand and depthwise records staged in LDS (else read from global memory)
     // LDS offsets: X1, E, D, records (start, expand, depthwise, project), add
     // tables, post tables, position tables (start, expand, depthwise, add),
     // tap words (start, depthwise)
@@ -130,10 +131,11 @@ __global__ __launch_bounds__(64 * IB_WAVES) void k_uib(UibArgs a)
             const v4i xzv = {xzw, xzw, xzw, xzw};
             for (int q = tid; q < (a.Ce >> 4) * planeE; q += NT) ((v4i *)E)[q] = xzv;
         }
-        for (int i = tid; i < 2 * a.Ce; i += NT) {
-            ((int4 *)(smem + a.o_re))[i] = a.epi_e[i];
-            if (K) ((int4 *)(smem + a.o_rd))[i] = a.epi_d[i];
-        }
+        if (a.rec_lds)
+            for (int i = tid; i < 2 * a.Ce; i += NT) {
+                ((int4 *)(smem + a.o_re))[i] = a.epi_e[i];
+                if (K) ((int4 *)(smem + a.o_rd))[i] = a.epi_d[i];
+            }
         for (int i = tid; i < 2 * a.Cout; i += NT) ((int4 *)(smem + a.o_rp))[i] = a.epi_p[i];
         if (K0) {
             for (int i = tid; i < 2 * a.Cin; i += NT) ((int4 *)(smem + a.o_r0))[i] = a.epi0[i];
@@ -179,16 +181,17 @@ __global__ __launch_bounds__(64 * IB_WAVES) void k_uib(UibArgs a)
     {
         const int8_t *src = K0 ? X1 : X;
         const int ss = K0 ? a.x1s : a.xs;
+        const int4 *rec = a.rec_lds ? (const int4 *)(smem + a.o_re) : a.epi_e;
         v4i wfe[8];
         int wfe_ct = -1;
         if (K) {
-            ib_gemm_mode<8>(a.e_mode, smem, wfe, wfe_ct, a.we, a.kpe, a.Cin >> 5, src, ss, Pe, a.Ce >> 5, a.o_re,
+            ib_gemm_mode<8>(a.e_mode, wfe, wfe_ct, a.we, a.kpe, a.Cin >> 5, src, ss, Pe, a.Ce >> 5, rec,
                             a.e_yz, a.e_lo, a.e_hi, a.lut_e ? lut_s : nullptr, [&](int p, int c, int word) {
                                 const int pos = te[p];
                                 if (pos >= 0) *(int *)(E + (__mul24(c >> 4, planeE) + pos) * 16 + (c & 15)) = word;
                             });
         } else {
-            ib_gemm_mode<8>(a.e_mode, smem, wfe, wfe_ct, a.we, a.kpe, a.Cin >> 5, src, ss, Pe, a.Ce >> 5, a.o_re,
+            ib_gemm_mode<8>(a.e_mode, wfe, wfe_ct, a.we, a.kpe, a.Cin >> 5, src, ss, Pe, a.Ce >> 5, rec,
                             a.e_yz, a.e_lo, a.e_hi, a.lut_e ? lut_s : nullptr,
                             [&](int p, int c, int word) { *(int *)(D + __mul24(p, a.ds) + c) = word; });
         }
@@ -197,8 +200,8 @@ __global__ __launch_bounds__(64 * IB_WAVES) void k_uib(UibArgs a)
 
     // Phase 3: depthwise into D.
     if constexpr (K > 0) {
-        const DwPh g = {Po, a.Ce, a.ds, a.cols_p, 0, a.d_yz, a.d_lo, a.d_hi, (const int4 *)(smem + a.o_rd),
-                        a.lut_d ? lut_s + 256 : nullptr};
+        const DwPh g = {Po, a.Ce, a.ds, a.cols_p, 0, a.d_yz, a.d_lo, a.d_hi,
+                        a.rec_lds ? (const int4 *)(smem + a.o_rd) : a.epi_d, a.lut_d ? lut_s + 256 : nullptr};
         ib_dw_mode<K>(a.d_mode, g, E, D, td, (const int *)(smem + a.o_wd), planeE);
         __syncthreads();
     }
@@ -234,11 +237,13 @@ __global__ __launch_bounds__(64 * IB_WAVES) void k_uib(UibArgs a)
     if ((i32 + IB_WAVES - 1) / IB_WAVES * 16 <= (i16 + IB_WAVES - 1) / IB_WAVES * 4) {
         v4i wfp[16];
         int wfp_ct = -1;
-        ib_gemm_mode<16>(a.p_mode, smem, wfp, wfp_ct, a.wp, a.kpp, a.Ce >> 5, D, a.ds, Po, a.Cout >> 5, a.o_rp,
-                         a.p_yz, a.p_lo, a.p_hi, a.lut_p ? lut_s + 512 : nullptr, project_sink);
+        ib_gemm_mode<16>(a.p_mode, wfp, wfp_ct, a.wp, a.kpp, a.Ce >> 5, D, a.ds, Po, a.Cout >> 5,
+                         (const int4 *)(smem + a.o_rp), a.p_yz, a.p_lo, a.p_hi, a.lut_p ? lut_s + 512 : nullptr,
+                         project_sink);
     } else {
-        ib_gemm16_mode<8>(a.p_mode, smem, a.wp, a.kpp, (a.Ce + 63) >> 6, D, a.ds, Po, a.Cout >> 4, a.o_rp, a.p_yz,
-                          a.p_lo, a.p_hi, a.lut_p ? lut_s + 512 : nullptr, project_sink);
+        ib_gemm16_mode<8>(a.p_mode, a.wp, a.kpp, (a.Ce + 63) >> 6, D, a.ds, Po, a.Cout >> 4,
+                          (const int4 *)(smem + a.o_rp), a.p_yz, a.p_lo, a.p_hi, a.lut_p ? lut_s + 512 : nullptr,
+                          project_sink);
     }
     __syncthreads();
     int8_t *yim = a.y + ((long)n * a.Ho + r0) * a.Wo * a.Cout;
@@ -247,8 +252,9 @@ __global__ __launch_bounds__(64 * IB_WAVES) void k_uib(UibArgs a)
 
 static size_t up16(size_t v) { return (v + 15) & ~(size_t)15; }
 
-// LDS layout for bands of R output rows; 0 when the block does not fit.
-static size_t uib_layout(const UQKUib *f, int R, UibArgs *t)
+// LDS layout for bands of R output rows, with the expand and depthwise
+// records in LDS or not; 0 when the block does not fit.
+static size_t uib_layout(const UQKUib *f, int R, int rec_lds, UibArgs *t)
 {
     const int K0 = f->k0, K = f->k, s = K ? f->s : 1;
     // Expanded rows a band needs, and those inside the map, at most.
@@ -263,8 +269,8 @@ static size_t uib_layout(const UQKUib *f, int R, UibArgs *t)
     t->o_e = (int)o; o += up16(K ? (size_t)(f->Ce / 16) * re * cols_p * 16 : 0);
     t->o_d = (int)o; o += up16((K ? Po : Pe) * (f->Ce + 16)) + 64;   // + the 16x16 project's K-tail over-read
     t->o_r0 = (int)o; o += K0 ? (size_t)f->Cin * 32 : 0;
-    t->o_re = (int)o; o += (size_t)f->Ce * 32;
-    t->o_rd = (int)o; o += K ? (size_t)f->Ce * 32 : 0;
+    t->o_re = (int)o; o += rec_lds ? (size_t)f->Ce * 32 : 0;
+    t->o_rd = (int)o; o += rec_lds && K ? (size_t)f->Ce * 32 : 0;
     t->o_rp = (int)o; o += (size_t)f->Cout * 32;
     t->o_at = (int)o; o += f->has_add ? 512 * 4 : 0;
     t->o_lut = (int)o; o += 4 * 256;
@@ -279,6 +285,7 @@ static size_t uib_layout(const UQKUib *f, int R, UibArgs *t)
     if (Po * f->Cout > stage) return 0;
     t->cols0 = cols0;
     t->cols_p = cols_p;
+    t->rec_lds = rec_lds;
     return o <= (size_t)UIB_LDS_MAX ? o : 0;
 }
 
@@ -300,14 +307,19 @@ extern "C" size_t uqk_uib_plan(UQKUib *f)
         return 0;
     }
     if (f->has_add && (f->Ho != f->H || f->Wo != f->W || f->Cin != f->Cout || (K && f->s != 1))) return 0;
+    // The most rows per band that fit, with the expand and depthwise records
+    // in LDS if they fit too (else read from L2 when a channel tile
+    // changes).
     UibArgs t;
-    for (int R = f->Ho; R >= 1; R--) {
-        const size_t lds = uib_layout(f, R, &t);
-        if (lds) {
-            f->R = R;
-            return lds;
+    for (int R = f->Ho; R >= 1; R--)
+        for (int rec_lds = 1; rec_lds >= 0; rec_lds--) {
+            const size_t lds = uib_layout(f, R, rec_lds, &t);
+            if (lds) {
+                f->R = R;
+                f->rec_lds = rec_lds;
+                return lds;
+            }
         }
-    }
     return 0;
 }
 
@@ -341,7 +353,7 @@ extern "C" int uqk_uib(const UQKUib *f, const void *x, void *y, uint32_t images)
     UQKUib g = *f;
     const int R = f->R;
     if (R < 1 || R > f->Ho || !uqk_uib_plan(&g) || R > g.R) return (int)hipErrorInvalidValue;
-    const size_t lds = uib_layout(f, R, &a);
+    const size_t lds = uib_layout(f, R, f->rec_lds, &a);
     if (!lds) return (int)hipErrorInvalidValue;
     a.bands = (f->Ho + R - 1) / R;
     const unsigned long long blocks = (unsigned long long)images * a.bands;

@@ -101,10 +101,12 @@ typedef struct {
     const void *add_tab;
     int32_t a_m, a_s, a_yz, a_lo, a_hi;
     int32_t R;                 /* output rows per band: set by uqk_uib_plan */
+    int32_t rec_lds;           /* expand and depthwise records in LDS: set by uqk_uib_plan */
 } UQKUib;
 
-/* Sets f->R to the most output rows per band whose workgroup fits in LDS and
- * returns that LDS size; 0 (and R = 0) when the block does not fit the
+/* Sets f->R to the most output rows per band whose workgroup fits in LDS
+ * (and f->rec_lds: whether the expand and depthwise records fit in LDS too)
+ * and returns that LDS size; 0 (and R = 0) when the block does not fit the
  * kernel (channel counts multiples of 32, Cin <= 256, Ce <= 512, pads within
  * the kernels, an add only at stride 1 with Cin == Cout). */
 size_t uqk_uib_plan(UQKUib *f);
