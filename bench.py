@@ -16,7 +16,10 @@ Prints ONE JSON line. Besides the headline images/s it reports:
                 conv TOPS (1x1 head GEMM, 3x3 implicit GEMM, batch 512),
                 batch-1 1x1 conv latency, host-buffer throughput and latency,
                 depthwise HBM GB/s (four cases, batch 64); each with `frac`
-                against its bound (5.0 POP/s dense int8, or 8 TB/s)
+                against its bound (5.0 POP/s dense int8, or 8 TB/s);
+                mfma_ceiling: the int8 rate a register-only MFMA loop
+                sustains for as long as each GEMM launch, against which the
+                GEMMs also carry `frac_of_ceiling`
 With --library-gemm it only prints the vendor library's int8 GEMM timings on
 the same GEMM shapes.
 """
@@ -36,7 +39,7 @@ sys.path.insert(0, str(ROOT / "unoq-dsp_amd"))
 
 import uq_plan as P  # noqa: E402
 import uq_workloads as W  # noqa: E402
-from uq_native import DeviceBuffer, Graph, open_library  # noqa: E402
+from uq_native import DeviceBuffer, Graph, mfma_ceiling, open_library  # noqa: E402
 
 METRIC = "images/sec @ batch 256, MobileNetV4-S int8 224²; conv int8 TOPS + DW HBM GB/s"
 HBM_PEAK = 8.0e12          # bytes/s
@@ -256,7 +259,16 @@ def secondary(lib, steps):
     out["yolo"] = {"images": images, "ms": round(sec / steps * 1e3, 4), "images_per_s": round(images * steps / sec, 1),
                    "gops": round(sum(c["ops"] for c in costs) / 1e9, 2),
                    "frac": round(nbytes / (sec / steps) / HBM_PEAK, 4), "bound": "hbm (network bytes)"}
-    for name in ("head", "conv3x3"):
+    # The matrix cores' sustained rate on this device: a register-only MFMA
+    # loop launched back to back for about as long as each GEMM launch
+    # (short: the head's ~45 us; long: the 3x3's ~0.6 ms), so that the clock
+    # it holds under that load is the GEMM's.
+    ceiling = {}
+    for label, iters in (("short", 180), ("long", 2400)):
+        tops, us = mfma_ceiling(lib, iters, warmup=3, reps=steps)
+        ceiling[label] = {"tops": round(tops, 1), "launch_us": round(us, 1), "frac": round(tops * 1e12 / INT8_PEAK, 4)}
+    out["mfma_ceiling"] = ceiling
+    for name, leg in (("head", "short"), ("conv3x3", "long")):
         plan, images = W.WORKLOADS[name]()
         g = Graph(plan, lib)
         sec, per_op = time_device(lib, g, images, steps, 2)
@@ -264,7 +276,7 @@ def secondary(lib, steps):
         kernel_tops = ops / (per_op.sum() * 1e-9) / 1e12
         out[name] = {"images": images, "ms": round(sec / steps * 1e3, 4), "tops": round(ops / (sec / steps) / 1e12, 2),
                      "kernel_tops": round(kernel_tops, 2), "frac": round(kernel_tops * 1e12 / INT8_PEAK, 4),
-                     "bound": "mfma"}
+                     "frac_of_ceiling": round(kernel_tops / ceiling[leg]["tops"], 4), "bound": "mfma"}
     out["pointwise_b1"] = pointwise_latency(lib, steps)
     out["host_transfer"] = host_transfer(lib, max(steps // 2, 3))
     for name in ("dw3s1", "dw3s2", "dw5s1", "dw5s2"):

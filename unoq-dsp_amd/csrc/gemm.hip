@@ -715,3 +715,93 @@ extern "C" int uqk_gemm(const UQKSpatial *d, const void *x, void *y, uint32_t ba
     a.nblocks = (int)blocks;
     return d->mode != UQK_PW ? launch_tile<true>(tile, a, emode) : launch_tile<false>(tile, a, emode);
 }
+
+// ---------------------------------------------------------------------------
+// Matrix-core ceiling (a measurement hook, not part of the plan ABI): waves
+// that issue v_mfma_i32_32x32x32_i8 on register operands, eight independent
+// accumulators each, two waves per SIMD as in the GEMMs above, no memory
+// traffic inside the loop (eight rotates per eight MFMAs vary the operands). Launched back to back for as long as a
+// GEMM launch lasts, it gives the int8 rate the device sustains at the clock
+// it holds under that load: the most any of the GEMMs could reach.
+__device__ int uqk_ceiling_sink;   // external linkage, so the loop's result is not dead
+
+__global__ __launch_bounds__(256) void k_mfma_ceiling(int iters)
+{
+    v16i acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[j][r] = 0;
+    // Operand bytes from a multiplicative hash of the lane and block, rotated
+    // by one bit after every round, so that the matrix cores see changing
+    // data (their power, and so the clock the device holds, depends on it).
+    v4i a, b;
+    const unsigned seed = (threadIdx.x + 1u) * 0x9e3779b1u ^ (blockIdx.x + 1u) * 0x85ebca77u;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        a[k] = (int)(seed * (2u * k + 3u) + 0x27d4eb2fu * k);
+        b[k] = (int)(seed * (2u * k + 7u) ^ 0x165667b1u * (k + 1u));
+    }
+    for (int i = 0; i < iters; i++) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[j], 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            a[k] = (int)__builtin_rotateleft32((unsigned)a[k], 1);
+            b[k] = (int)__builtin_rotateleft32((unsigned)b[k], 1);
+        }
+    }
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) s += acc[j][r];
+    if (s == 0x7fffffff) uqk_ceiling_sink = s;    // keeps the loop; almost never stores
+}
+
+// Runs `warmup` untimed and `reps` timed launches of `iters` rounds on
+// every SIMD (two blocks of four waves per compute unit) on the library
+// stream and returns the sustained rate in *tops (10^12 int8 ops/s, two per
+// multiply-accumulate) and the mean launch time in *us.
+extern "C" int uqk_mfma_ceiling(int iters, int warmup, int reps, double *tops, double *us)
+{
+    if (iters < 1 || reps < 1 || warmup < 0 || !tops || !us) return (int)hipErrorInvalidValue;
+    if (!g_cus) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n < 1)
+            return uqk_fail(hipErrorInvalidDevice);
+        g_cus = n;
+    }
+    hipStream_t st;
+    hipEvent_t e0, e1;
+    uqk_next_launch(&st, &e0, &e1);
+    hipEvent_t t0, t1;
+    if (hipEventCreate(&t0) != hipSuccess) return uqk_fail(hipErrorOutOfMemory);
+    if (hipEventCreate(&t1) != hipSuccess) {
+        (void)hipEventDestroy(t0);
+        return uqk_fail(hipErrorOutOfMemory);
+    }
+    const dim3 grid((unsigned)(2 * g_cus)), block(256);
+    int rc = 0;
+    for (int i = 0; i < warmup && !rc; i++) {
+        hipLaunchKernelGGL(k_mfma_ceiling, grid, block, 0, st, iters);
+        rc = uqk_fail(hipGetLastError());
+    }
+    if (!rc) rc = uqk_fail(hipEventRecord(t0, st));
+    for (int i = 0; i < reps && !rc; i++) {
+        hipLaunchKernelGGL(k_mfma_ceiling, grid, block, 0, st, iters);
+        rc = uqk_fail(hipGetLastError());
+    }
+    if (!rc) rc = uqk_fail(hipEventRecord(t1, st));
+    if (!rc) rc = uqk_fail(hipEventSynchronize(t1));
+    float ms = 0.f;
+    if (!rc) rc = uqk_fail(hipEventElapsedTime(&ms, t0, t1));
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
+    if (rc) return rc;
+    const double ops = 2.0 * 32 * 32 * 32 * 8 * (double)iters * 4 * grid.x * reps;
+    *us = ms * 1e3 / reps;
+    *tops = ops / (ms * 1e-3) / 1e12;
+    return 0;
+}

@@ -70,7 +70,20 @@ def open_library(path=None):
     for hook in ("uqk_gemm_launches", "uqk_ib_launches", "uqk_stem_conv_launches", "uqk_uib_launches"):
         getattr(lib, hook).restype = C.c_uint64
         getattr(lib, hook).argtypes = []
+    # Measurement hook: the sustained int8 matrix-core rate of a register-only
+    # MFMA loop (iters, warm-up launches, timed launches -> TOP/s, us/launch).
+    lib.uqk_mfma_ceiling.restype = C.c_int
+    lib.uqk_mfma_ceiling.argtypes = [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]
     return lib
+
+
+def mfma_ceiling(lib, iters, warmup=3, reps=10):
+    """(TOP/s, us per launch) of the register-only int8 MFMA loop."""
+    tops, us = C.c_double(), C.c_double()
+    rc = lib.uqk_mfma_ceiling(iters, warmup, reps, C.byref(tops), C.byref(us))
+    if rc:
+        raise RuntimeError(f"uqk_mfma_ceiling failed: {rc}")
+    return tops.value, us.value
 
 
 class Graph:
