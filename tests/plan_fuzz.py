@@ -649,7 +649,7 @@ def stem_conv_plan(seed):
     conv over its output, the pair the fused stem kernel takes: SAME or
     explicit padding on both, strides 1-2 on the stem, widths from 16 to 96
     input columns, odd heights, post tables, all requantisation ranges, and
-    sometimes an op after the pair."""
+    sometimes a post-table op and/or a 1x1 32 -> 32 conv after the pair."""
     rng = Rng(seed, 929292)
     p = Plan(seed)
     ic = _pick(rng, [1, 2, 3, 3, 4])
@@ -683,4 +683,8 @@ def stem_conv_plan(seed):
     z = layer(lambda shift: p.conv(s, 32, k=3, stride=2, padding=padding, shift=shift, **opts()))
     if _pick(rng, [0, 1]):
         z = p.lut(z, _random_lut(p, rng))
+    # A 1x1 32 -> 32 conv after the pair: fused with it when it reads the
+    # 3x3's output directly, a separate launch after a post-table op.
+    if _pick(rng, [0, 1, 1]):
+        z = layer(lambda shift: p.conv(z, 32, k=1, shift=shift, **opts()))
     return p.build(z)

@@ -354,11 +354,13 @@ def test_mnv4_banded_groups(lib, monkeypatch, mode, launches):
 
 @pytest.mark.parametrize("seed", range(40))
 def test_stem_conv_fusion(lib, monkeypatch, seed):
-    """A stem conv and the 3x3 stride-2 conv over its output run as one
-    launch by default: one to three images match the oracle byte for byte,
-    as they do unfused (UQ_FUSE_STEM=0). After a host-buffer run a snapshot
-    of the stem's output is rebuilt; after a device-buffer run (the stem
-    read the caller's buffer) it is refused with 22."""
+    """A stem conv and the 3x3 stride-2 conv over its output (and a 1x1
+    32 -> 32 conv right after, when there is one) run as one launch by
+    default: one to three images match the oracle byte for byte, as they do
+    with the 1x1 apart (UQ_FUSE_STEM=2) and unfused (UQ_FUSE_STEM=0). After a
+    host-buffer run snapshots of the inner tensors are rebuilt; after a
+    device-buffer run (the stem read the caller's buffer) they are refused
+    with 22."""
     plan = stem_conv_plan(seed)
     images = 1 + seed % 3
     x = P.random_input(plan, images, seed)
@@ -367,18 +369,32 @@ def test_stem_conv_fusion(lib, monkeypatch, seed):
     before = lib.uqk_stem_conv_launches()
     _assert_same(g.run_batch(x, images), want, f"fused stem plan {seed}")
     assert lib.uqk_stem_conv_launches() > before, "the fused stem kernel did not run"
-    stem_out = P.op_records(plan)[0][3]
+    ops = P.op_records(plan)
+    stem_out = ops[0][3]
     nbytes = images * P.tensor_records(plan)[stem_out][1]
     _, snap = oracle_run(plan, x, images, P.output_bytes(plan), snap=stem_out, snap_bytes=nbytes)
     _assert_same(g.snapshot_images(stem_out, nbytes), snap, f"fused stem plan {seed}: stem output snapshot")
+    if len(ops) > 2 and ops[2][0] == 14 and ops[2][1] == ops[1][3]:
+        # The 1x1 ran in the same launch: the 3x3's output is rebuilt too.
+        g.run_batch(x, images)
+        mid = ops[1][3]
+        mbytes = images * P.tensor_records(plan)[mid][1]
+        _, msnap = oracle_run(plan, x, images, P.output_bytes(plan), snap=mid, snap_bytes=mbytes)
+        _assert_same(g.snapshot_images(mid, mbytes), msnap, f"fused stem plan {seed}: 3x3 output snapshot")
     din, dout = DeviceBuffer(lib, x.nbytes), DeviceBuffer(lib, images * g.output_bytes)
     din.upload(x)
     assert lib.ug_run_device(din.ptr, dout.ptr, images) == 0
     _assert_same(dout.download(), want, f"fused stem plan {seed}, device buffers")
     buf = np.empty(nbytes, np.int8)
     assert lib.ug_snapshot_images(stem_out, buf.ctypes.data, buf.nbytes) == 22
+    if len(ops) > 2 and ops[2][0] == 14 and ops[2][1] == ops[1][3]:
+        # The 3x3's output is inside the fused launch as well.
+        mbuf = np.empty(images * P.tensor_records(plan)[ops[1][3]][1], np.int8)
+        assert lib.ug_snapshot_images(ops[1][3], mbuf.ctypes.data, mbuf.nbytes) == 22
     din.free()
     dout.free()
+    monkeypatch.setenv("UQ_FUSE_STEM", "2")
+    _assert_same(Graph(plan, lib).run_batch(x, images), want, f"stem plan {seed}, 1x1 not fused")
     monkeypatch.setenv("UQ_FUSE_STEM", "0")
     before = lib.uqk_stem_conv_launches()
     _assert_same(Graph(plan, lib).run_batch(x, images), want, f"unfused stem plan {seed}")

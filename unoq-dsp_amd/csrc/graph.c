@@ -33,8 +33,8 @@ typedef struct { uint32_t code, a, b, out, p[4]; } Op;
 
 /* A fused group (see find_groups): an inverted bottleneck run by one launch
  * (kind 0), a conv whose residual add runs in its epilogue (kind 1), a stem
- * conv and the 3x3 stride-2 conv over its output (kind 2), or a banded
- * universal inverted bottleneck (kind 3). */
+ * conv, the 3x3 stride-2 conv over its output and optionally the 1x1 after
+ * that (kind 2), or a banded universal inverted bottleneck (kind 3). */
 typedef struct {
     int kind;
     UQKIb desc;
@@ -986,28 +986,34 @@ static uint32_t find_uib(uint32_t i, const uint16_t *users, int bands_ok)
     return nops;
 }
 
-/* Stem + 3x3 stride 2: a stem conv (the stem form, 32 output channels)
- * whose output, used by nothing else, is the input of the next op, a 3x3
- * stride-2 conv over those 32 channels that fits stem.hip. On unless
- * UQ_FUSE_STEM=0 at load time. */
-static int find_stem_conv(uint32_t i, const uint16_t *users)
+/* Stem + 3x3 stride 2 [+ 1x1]: a stem conv (the stem form, 32 output
+ * channels) whose output, used by nothing else, is the input of the next op,
+ * a 3x3 stride-2 conv over those 32 channels that fits stem.hip; and when
+ * the op after that is a 1x1 32 -> 32 conv over the 3x3's output, used by
+ * nothing else either, that conv too. On unless UQ_FUSE_STEM=0 at load
+ * time (UQ_FUSE_STEM=2: stem and 3x3 only). Returns the ops taken. */
+static int find_stem_conv(uint32_t i, const uint16_t *users, int with_pw)
 {
     const Op *s = G.ops + i, *c = G.ops + i + 1;
     if (s->code != 14 || c->code != 14 || c->a != s->out) return 0;
     const uint32_t t = s->out;
     if (users[t] != 1 || t == G.h.output || G.ts[s->a].rank != 4 || G.ts[s->a].d[0] != 1) return 0;
-    if (!uqk_stem_conv_ok(G.sp + i, G.sp + i + 1)) return 0;
+    if (!uqk_stem_conv_ok(G.sp + i, G.sp + i + 1, NULL)) return 0;
+    const Op *p = i + 2 < G.h.no ? G.ops + i + 2 : NULL;
+    const int pw = with_pw && p && p->code == 14 && p->a == c->out && users[c->out] == 1 && c->out != G.h.output &&
+                   uqk_stem_conv_ok(G.sp + i, G.sp + i + 1, G.sp + i + 2);
     Group *g = &G.groups[G.ngroups];
     memset(g, 0, sizeof *g);
     g->kind = 2;
     g->first = i;
-    g->nops = 2;
+    g->nops = pw ? 3 : 2;
     g->in = s->a;
-    g->out = c->out;
+    g->out = pw ? p->out : c->out;
     G.fuse_at[i] = (uint16_t)(G.ngroups + 1);
     G.fuse_of_tensor[t] = (uint16_t)(G.ngroups + 1);
+    if (pw) G.fuse_of_tensor[c->out] = (uint16_t)(G.ngroups + 1);
     G.ngroups++;
-    return 1;
+    return (int)g->nops;
 }
 
 static void find_groups(void)
@@ -1023,11 +1029,11 @@ static void find_groups(void)
     const char *env = getenv("UQ_FUSE_BOTTLENECK");
     const int bottleneck = !(env && !strcmp(env, "0"));
     const char *senv = getenv("UQ_FUSE_STEM");
-    const int stem = !(senv && !strcmp(senv, "0"));
+    const int stem = !(senv && !strcmp(senv, "0")), stem_pw = !(senv && !strcmp(senv, "2"));
     const char *uenv = getenv("UQ_FUSE_UIB");
     const int uib = !uenv ? 1 : !strcmp(uenv, "0") ? 0 : !strcmp(uenv, "2") ? 2 : 1;
     for (uint32_t i = 0; i + 1 < G.h.no; i++) {
-        uint32_t n = stem && find_stem_conv(i, users) ? 2 : 0;
+        uint32_t n = stem ? (uint32_t)find_stem_conv(i, users, stem_pw) : 0;
         if (!n && uib) n = find_uib(i, users, uib);
         if (!n && bottleneck) n = find_bottleneck(i, users);
         if (!n && find_conv_add(i, users)) n = 2;
@@ -1194,7 +1200,8 @@ static int enqueue_range(uint32_t i0, uint32_t i1, uint32_t images, uint32_t *ne
                 rc = uqk_conv_add(G.sp + i, G.ptr[grp->in], G.ptr[grp->out], images * G.ts[G.ops[i].a].d[0],
                                   &grp->add);
             } else {
-                rc = uqk_stem_conv(G.sp + i, G.sp + i + 1, G.ptr[grp->in], G.ptr[grp->out], images);
+                rc = uqk_stem_conv(G.sp + i, G.sp + i + 1, grp->nops == 3 ? G.sp + i + 2 : NULL, G.ptr[grp->in],
+                                   G.ptr[grp->out], images);
             }
             if (rc) return rc;
             grp->last_in = G.ptr[grp->in];

@@ -23,14 +23,21 @@
 //      zero); the weights as the MFMA rows, held in registers for the whole
 //      phase; the requantised words of four row blocks transposed across
 //      16-lane rows (rows_transpose4) into one 16-byte store per lane.
-// Both epilogues use the layers' own records and requantisation, so the
-// bytes equal the two separate launches'.
+//   3  (optional) a 1x1 conv over 32 channels after the 3x3, whose input
+//      is nothing else's: a lane's 32 channels of the 3x3's output (one
+//      pixel per lane after phase 2's transpose) become the pixel operand of
+//      v_mfma_i32_32x32x32_i8 (one v_permlane32_swap per register pair), the
+//      1x1's weights its other operand, and only the 1x1's output is stored.
+// Every epilogue uses its layer's own records and requantisation, so the
+// bytes equal the separate launches'.
 #include <hip/hip_runtime.h>
 #include <hip/hip_ext.h>
 #include <stdint.h>
 #include "uqk.h"
 #include "uqk_device.h"
 #include "uqk_internal.h"
+
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int SC_NT = 2;            // 32 channels in both layers (two 16-channel tiles)
 constexpr int SC_C = 32;
@@ -57,17 +64,66 @@ struct StemConvArgs {
     int cpr;                   // 16-byte pieces per staged row (the last is the gap)
     unsigned m_cpr, m_ow;      // udiv_magic(cpr), udiv_magic(c_ow)
     int cols;                  // columns of S: (c_ow - 1) * 2 + 3
-    int o_s, o_es, o_ec, o_ls, o_lc;   // LDS offsets: S, stem records, conv records, post tables
+    int o_s, o_es, o_ec, o_ls, o_lc, o_lp;   // LDS offsets: S, stem records, conv records, post tables
+    // optional 1x1 conv over the 3x3's output (32 -> 32 channels): weights
+    // [>= 32][p_kpad], its records, post table and requantisation variant
+    const int8_t *wp;
+    const int4 *epip;
+    const uint8_t *lutp;
+    int p_kpad, p_mode, p_yz, p_lo, p_hi;
 };
 
-template <int EMS, int EMC>
+// The 1x1 conv over 64 pixels of the 3x3's output, lane L holding the 32
+// channels of pixel L as h0 (channels 0-15) and h1 (16-31): one
+// v_permlane32_swap per register pair gives the two 32-pixel A operands of
+// v_mfma_i32_32x32x32_i8 (rows: pixels, K: lanes < 32 channels 0-15, the
+// others 16-31); the weights are its columns (lane: output channel
+// lane & 31, K half lane >> 5), so a lane's 16 results share one channel and
+// its record; a 4x4 byte transpose across lane quads gives each lane four
+// channels of one pixel, stored as one word.
+template <bool HI, bool CORR>
+__device__ __forceinline__ void stem_pw(const StemConvArgs &a, const int (&h0)[4], const int (&h1)[4], const v4i &wpf,
+                                        const Epi &ep, const int8_t *lut_p, int8_t *yg, int px0, int npx)
+{
+    const int lane = threadIdx.x & 63, fr = lane & 31, fh = lane >> 5;
+    const int vlo = vgpr(a.p_lo), vhi = vgpr(a.p_hi);
+    v4i A[2];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(h0[j], h1[j], false, false);
+        A[0][j] = (int)sw[0];
+        A[1][j] = (int)sw[1];
+    }
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        v16i acc;
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[r] = 0;
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[t], wpf, acc, 0, 0, 0);
+        // acc[4g + i]: pixel px0 + 32t + 8g + 4fh + i, channel fr.
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            int v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[i] = conv_requant<HI, CORR>(acc[4 * g + i], ep, a.p_yz, vlo, vhi);
+                if (a.lutp) v[i] = lut_p[v[i] + 128];
+            }
+            const int word = quad_transpose_bytes(pack4(v[0], v[1], v[2], v[3]), lane);
+            const int px = px0 + 32 * t + 8 * g + 4 * fh + (lane & 3);
+            if (px < npx) *(int *)(yg + __mul24(px, SC_C) + (fr & ~3)) = word;
+        }
+    }
+}
+
+template <int EMS, int EMC, bool PW>
 __global__ __launch_bounds__(256) void k_stem_conv(StemConvArgs a)
 {
     constexpr bool HS = EMS & 1, CS = EMS & 2, HC = EMC & 1, CC = EMC & 2;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     int8_t *S = smem + a.o_s;
     const int4 *es = (const int4 *)(smem + a.o_es), *ec = (const int4 *)(smem + a.o_ec);
-    const int8_t *lut_s = smem + a.o_ls, *lut_c = smem + a.o_lc;
+    const int8_t *lut_s = smem + a.o_ls, *lut_c = smem + a.o_lc, *lut_p = smem + a.o_lp;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lg = lane >> 4;
     const int n = blockIdx.x / a.bands, band = blockIdx.x - n * a.bands;
@@ -118,6 +174,7 @@ __global__ __launch_bounds__(256) void k_stem_conv(StemConvArgs a)
         if (tid < 64) {
             if (a.luts) ((int *)lut_s)[tid] = ((const int *)a.luts)[tid];
             if (a.lutc) ((int *)lut_c)[tid] = ((const int *)a.lutc)[tid];
+            if (PW && a.lutp) ((int *)lut_p)[tid] = ((const int *)a.lutp)[tid];
         }
     }
     __syncthreads();
@@ -177,6 +234,12 @@ __global__ __launch_bounds__(256) void k_stem_conv(StemConvArgs a)
         }
         const int npx = brows * a.c_ow, groups = (npx + 63) >> 6;
         int8_t *ybase = a.y + ((long)n * a.c_oh + r0) * a.c_ow * SC_C;
+        v4i wpf = {0, 0, 0, 0};
+        Epi ep = {};
+        if (PW) {
+            wpf = *(const v4i *)(a.wp + (long)(lane & 31) * a.p_kpad + (lane >> 5) * 16);
+            ep = load_epi(a.epip, lane & 31);
+        }
         for (int g = wave; g < groups; g += 4) {
             v4i acc[4][SC_NT];
 #pragma unroll
@@ -195,6 +258,7 @@ __global__ __launch_bounds__(256) void k_stem_conv(StemConvArgs a)
                 }
             }
             // acc[rb][nt][i]: channel nt*16 + 4*lg + i of pixel g*64 + rb*16 + lr.
+            int h[SC_NT][4];
 #pragma unroll
             for (int nt = 0; nt < SC_NT; nt++) {
                 Epi e[4];
@@ -214,10 +278,29 @@ __global__ __launch_bounds__(256) void k_stem_conv(StemConvArgs a)
                 rows_transpose4(r);
                 // Lane (lr, lg) now holds the 16 channels of pixel g*64 + lg*16 + lr.
                 const int px = g * 64 + lg * 16 + lr;
-                if (px < npx) *(v4i *)(ybase + __mul24(px, SC_C) + nt * 16) = (v4i){r[0], r[1], r[2], r[3]};
+                if (!PW && px < npx) *(v4i *)(ybase + __mul24(px, SC_C) + nt * 16) = (v4i){r[0], r[1], r[2], r[3]};
+#pragma unroll
+                for (int q = 0; q < 4; q++) h[nt][q] = r[q];
+            }
+            if (PW) {
+                switch (a.p_mode) {
+                case 0: stem_pw<false, false>(a, h[0], h[1], wpf, ep, lut_p, ybase, g * 64, npx); break;
+                case 1: stem_pw<true, false>(a, h[0], h[1], wpf, ep, lut_p, ybase, g * 64, npx); break;
+                case 2: stem_pw<false, true>(a, h[0], h[1], wpf, ep, lut_p, ybase, g * 64, npx); break;
+                default: stem_pw<true, true>(a, h[0], h[1], wpf, ep, lut_p, ybase, g * 64, npx); break;
+                }
             }
         }
     }
+}
+
+// Whether a 1x1 conv over the 3x3's output fits phase 3: 32 -> 32 channels,
+// stride 1, no padding or dilation, weights rows of 32 (or more, zero) bytes.
+static int sc_pw_fits(const UQKSpatial *c, const UQKSpatial *p)
+{
+    return p->mode == UQK_PW && p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->pt == 0 && p->pl == 0 &&
+           p->ic == SC_C && p->oc == SC_C && p->oc_pad >= SC_C && p->K == SC_C && p->kpad >= SC_C &&
+           p->ih == c->oh && p->iw == c->ow && p->oh == c->oh && p->ow == c->ow;
 }
 
 // Block geometry and LDS bytes; 0 when the pair does not fit the kernel.
@@ -242,6 +325,7 @@ static size_t sc_plan(const UQKSpatial *s, const UQKSpatial *c, int br, StemConv
     t->o_ec = (int)o; o += SC_C * 32;
     t->o_ls = (int)o; o += 256;
     t->o_lc = (int)o; o += 256;
+    t->o_lp = (int)o; o += 256;
     return o <= (size_t)SC_LDS_MAX ? o : 0;
 }
 
@@ -251,10 +335,10 @@ static size_t sc_plan(const UQKSpatial *s, const UQKSpatial *c, int br, StemConv
 // more LDS per block).
 static const int SC_BR = 3;
 
-extern "C" int uqk_stem_conv_ok(const UQKSpatial *s, const UQKSpatial *c)
+extern "C" int uqk_stem_conv_ok(const UQKSpatial *s, const UQKSpatial *c, const UQKSpatial *p)
 {
     StemConvArgs t;
-    return uqk_conv_stem_ok(s) && sc_plan(s, c, SC_BR, &t) > 0;
+    return uqk_conv_stem_ok(s) && sc_plan(s, c, SC_BR, &t) > 0 && (!p || sc_pw_fits(c, p));
 }
 
 static uint64_t g_sc_launches;
@@ -263,12 +347,13 @@ static uint64_t g_sc_launches;
 // hook; not part of the plan ABI).
 extern "C" uint64_t uqk_stem_conv_launches(void) { return g_sc_launches; }
 
-extern "C" int uqk_stem_conv(const UQKSpatial *s, const UQKSpatial *c, const void *x, void *y, uint32_t images)
+extern "C" int uqk_stem_conv(const UQKSpatial *s, const UQKSpatial *c, const UQKSpatial *p, const void *x, void *y,
+                             uint32_t images)
 {
     if (!images) return 0;
     StemConvArgs a;
     const size_t lds = sc_plan(s, c, SC_BR, &a);
-    if (!lds || !uqk_conv_stem_ok(s)) return (int)hipErrorInvalidValue;
+    if (!lds || !uqk_conv_stem_ok(s) || (p && !sc_pw_fits(c, p))) return (int)hipErrorInvalidValue;
     const unsigned long long blocks = (unsigned long long)images * a.bands;
     if (blocks > 0x7fffffffULL || (unsigned long long)s->ih * s->iw * s->ic > 0x7fffffffULL)
         return (int)hipErrorInvalidValue;
@@ -282,12 +367,23 @@ extern "C" int uqk_stem_conv(const UQKSpatial *s, const UQKSpatial *c, const voi
     a.c_yz = c->yz; a.c_lo = c->lo; a.c_hi = c->hi;
     a.m_cpr = udiv_magic((unsigned)a.cpr);
     a.m_ow = udiv_magic((unsigned)c->ow);
+    a.wp = nullptr; a.epip = nullptr; a.lutp = nullptr;
+    a.p_kpad = a.p_mode = a.p_yz = a.p_lo = a.p_hi = 0;
+    if (p) {
+        a.wp = (const int8_t *)p->w; a.epip = (const int4 *)p->epi; a.lutp = (const uint8_t *)p->lut;
+        a.p_kpad = p->kpad; a.p_mode = (p->hi_shift ? 1 : 0) | (p->corr ? 2 : 0);
+        a.p_yz = p->yz; a.p_lo = p->lo; a.p_hi = p->hi;
+    }
     const int ems = (s->hi_shift ? 1 : 0) | (s->corr ? 2 : 0), emc = (c->hi_shift ? 1 : 0) | (c->corr ? 2 : 0);
     hipStream_t st;
     hipEvent_t e0, e1;
     uqk_next_launch(&st, &e0, &e1);
     const dim3 grid((unsigned)blocks), block(256);
-#define SC_L(S, C) hipExtLaunchKernelGGL((k_stem_conv<S, C>), grid, block, (uint32_t)lds, st, e0, e1, 0u, a)
+#define SC_L(S, C)                                                                                              \
+    do {                                                                                                        \
+        if (p) hipExtLaunchKernelGGL((k_stem_conv<S, C, true>), grid, block, (uint32_t)lds, st, e0, e1, 0u, a); \
+        else hipExtLaunchKernelGGL((k_stem_conv<S, C, false>), grid, block, (uint32_t)lds, st, e0, e1, 0u, a);  \
+    } while (0)
 #define SC_EMC(S)                       \
     do {                                \
         switch (emc) {                  \

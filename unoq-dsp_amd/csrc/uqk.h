@@ -113,10 +113,12 @@ size_t uqk_uib_plan(UQKUib *f);
 int uqk_uib(const UQKUib *f, const void *x, void *y, uint32_t images);
 
 /* Stem conv fused with the 3x3 stride-2 conv over its 32-channel output
- * (stem.hip): whether the pair fits, and its launch (images of the stem's
- * input to the 3x3's output). */
-int uqk_stem_conv_ok(const UQKSpatial *s, const UQKSpatial *c);
-int uqk_stem_conv(const UQKSpatial *s, const UQKSpatial *c, const void *x, void *y, uint32_t images);
+ * and, when p is not null, the 1x1 32 -> 32 conv over the 3x3's output
+ * (stem.hip): whether the group fits, and its launch (images of the stem's
+ * input to the last conv's output). */
+int uqk_stem_conv_ok(const UQKSpatial *s, const UQKSpatial *c, const UQKSpatial *p);
+int uqk_stem_conv(const UQKSpatial *s, const UQKSpatial *c, const UQKSpatial *p, const void *x, void *y,
+                  uint32_t images);
 
 /* Whether a conv layer fits the stem kernel (kh <= 4, kw * IC <= 16, no
  * column dilation, left and right padding within 16 bytes, input rows a
