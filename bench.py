@@ -332,9 +332,17 @@ def main():
     ap.add_argument("--images", type=int, default=0, help="batch size (default: the workload's own)")
     ap.add_argument("--library-gemm", action="store_true",
                     help="only time the vendor library's int8 GEMM on the same shapes and print it as JSON")
+    ap.add_argument("--mfma-ceiling", type=int, default=0, metavar="ITERS",
+                    help="only time the register-only int8 MFMA loop (ITERS rounds per wave, --steps launches "
+                         "after --warmup) and print it as JSON")
     args = ap.parse_args()
     if args.library_gemm:
         print(json.dumps(library_gemm()), flush=True)
+        return
+    if args.mfma_ceiling:
+        tops, us = mfma_ceiling(open_library(), args.mfma_ceiling, warmup=args.warmup, reps=args.steps)
+        print(json.dumps({"mfma_ceiling": {"iters": args.mfma_ceiling, "tops": round(tops, 1), "launch_us": round(us, 1),
+                                           "frac": round(tops * 1e12 / INT8_PEAK, 4)}}), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); images are independent, so N GPUs "
