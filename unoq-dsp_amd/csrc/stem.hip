@@ -116,8 +116,11 @@ __device__ __forceinline__ void stem_pw(const StemConvArgs &a, const int (&h0)[4
     }
 }
 
-template <int EMS, int EMC, bool PW>
-__global__ __launch_bounds__(256) void k_stem_conv(StemConvArgs a)
+// WPE: the waves per SIMD the register allocation must allow (1: no limit).
+// Four let four blocks share a compute unit; the host takes that variant
+// only when it compiled without spilling (uqk_stem_conv).
+template <int EMS, int EMC, bool PW, int WPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void k_stem_conv(StemConvArgs a)
 {
     constexpr bool HS = EMS & 1, CS = EMS & 2, HC = EMC & 1, CC = EMC & 2;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
@@ -131,8 +134,9 @@ __global__ __launch_bounds__(256) void k_stem_conv(StemConvArgs a)
     const int s0 = r0 * 2 - a.c_pt;                    // stem row of S row 0
     const int iy_base = s0 * a.s_sh - a.s_pt;          // input row of staged row 0
 
-    // Stem weights (MFMA rows: channel nt*16 + lr, kernel row lg) and the
-    // 3x3's weights for all five K steps, loaded while the block stages.
+    // Stem weights (MFMA rows: channel nt*16 + lr, kernel row lg), the 3x3's
+    // weights for all five K steps and the 1x1's, loaded while the block
+    // stages.
     v4i wsf[SC_NT];
 #pragma unroll
     for (int nt = 0; nt < SC_NT; nt++) wsf[nt] = *(const v4i *)(a.ws + (long)(nt * 16 + lr) * 64 + lg * 16);
@@ -141,6 +145,14 @@ __global__ __launch_bounds__(256) void k_stem_conv(StemConvArgs a)
     for (int nt = 0; nt < SC_NT; nt++)
 #pragma unroll
         for (int s = 0; s < 5; s++) wcf[nt][s] = *(const v4i *)(a.wc + (long)(nt * 16 + lr) * a.c_kpad + s * 64 + lg * 16);
+    // The 1x1's weights (its MFMA columns: channel lane & 31, K half lane >> 5)
+    // and its channel's record.
+    v4i wpf = {0, 0, 0, 0};
+    Epi ep = {};
+    if (PW) {
+        wpf = *(const v4i *)(a.wp + (long)(lane & 31) * a.p_kpad + (lane >> 5) * 16);
+        ep = load_epi(a.epip, lane & 31);
+    }
 
     // Phase 0.
     {
@@ -234,12 +246,6 @@ __global__ __launch_bounds__(256) void k_stem_conv(StemConvArgs a)
         }
         const int npx = brows * a.c_ow, groups = (npx + 63) >> 6;
         int8_t *ybase = a.y + ((long)n * a.c_oh + r0) * a.c_ow * SC_C;
-        v4i wpf = {0, 0, 0, 0};
-        Epi ep = {};
-        if (PW) {
-            wpf = *(const v4i *)(a.wp + (long)(lane & 31) * a.p_kpad + (lane >> 5) * 16);
-            ep = load_epi(a.epip, lane & 31);
-        }
         for (int g = wave; g < groups; g += 4) {
             v4i acc[4][SC_NT];
 #pragma unroll
@@ -343,6 +349,23 @@ extern "C" int uqk_stem_conv_ok(const UQKSpatial *s, const UQKSpatial *c, const 
 
 static uint64_t g_sc_launches;
 
+// Launch the four-waves-per-SIMD variant of a kernel instance when it needs
+// no scratch memory (no spilled registers), else the unrestricted one; the
+// choice is made once per instance.
+template <int EMS, int EMC, bool PW>
+static void sc_launch(dim3 grid, dim3 block, size_t lds, hipStream_t st, hipEvent_t e0, hipEvent_t e1,
+                      const StemConvArgs &a)
+{
+    static int use4 = -1;
+    if (use4 < 0) {
+        hipFuncAttributes fa;
+        use4 = hipFuncGetAttributes(&fa, (const void *)k_stem_conv<EMS, EMC, PW, 4>) == hipSuccess &&
+               fa.localSizeBytes == 0;
+    }
+    if (use4) hipExtLaunchKernelGGL((k_stem_conv<EMS, EMC, PW, 4>), grid, block, (uint32_t)lds, st, e0, e1, 0u, a);
+    else hipExtLaunchKernelGGL((k_stem_conv<EMS, EMC, PW, 1>), grid, block, (uint32_t)lds, st, e0, e1, 0u, a);
+}
+
 // Launches of the fused stem kernel since the library was loaded (a test
 // hook; not part of the plan ABI).
 extern "C" uint64_t uqk_stem_conv_launches(void) { return g_sc_launches; }
@@ -379,10 +402,10 @@ extern "C" int uqk_stem_conv(const UQKSpatial *s, const UQKSpatial *c, const UQK
     hipEvent_t e0, e1;
     uqk_next_launch(&st, &e0, &e1);
     const dim3 grid((unsigned)blocks), block(256);
-#define SC_L(S, C)                                                                                              \
-    do {                                                                                                        \
-        if (p) hipExtLaunchKernelGGL((k_stem_conv<S, C, true>), grid, block, (uint32_t)lds, st, e0, e1, 0u, a); \
-        else hipExtLaunchKernelGGL((k_stem_conv<S, C, false>), grid, block, (uint32_t)lds, st, e0, e1, 0u, a);  \
+#define SC_L(S, C)                                                                    \
+    do {                                                                              \
+        if (p) sc_launch<S, C, true>(grid, block, lds, st, e0, e1, a);                \
+        else sc_launch<S, C, false>(grid, block, lds, st, e0, e1, a);                 \
     } while (0)
 #define SC_EMC(S)                       \
     do {                                \
