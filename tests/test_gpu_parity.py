@@ -596,6 +596,20 @@ def test_depthwise_kernels(lib, kernel, seed, monkeypatch):
     _assert_same(Graph(plan, lib).run_batch(x, images), _oracle(plan, x, images), f"depthwise {kernel} {seed}")
 
 
+@pytest.mark.parametrize("rows,seed", [(1, 0), (2, 1), (3, 2), (5, 3), (7, 4), (1, 5), (4, 6), (6, 7)])
+def test_depthwise_window_bands(lib, rows, seed, monkeypatch):
+    """The matrix-core window depthwise with its blocks forced to at most
+    `rows` output rows (UQ_DW_ROWS), one to three images, byte for byte
+    against the oracle (unforced, these small launches split their maps into
+    equal bands of the launch's own choice: test_depthwise_kernels)."""
+    monkeypatch.setenv("UQ_DW", "mfma")
+    monkeypatch.setenv("UQ_DW_ROWS", str(rows))
+    plan = dw_mfma_plan(200 + seed)
+    images = 1 + seed % 3
+    x = P.random_input(plan, images, seed)
+    _assert_same(Graph(plan, lib).run_batch(x, images), _oracle(plan, x, images), f"depthwise bands {rows} {seed}")
+
+
 def test_profile_counts_one_run_per_profiled_batch(lib):
     """ug_profile counters count finished profiled batches: a synchronize
     with none pending adds nothing; one device run adds one; two enqueues

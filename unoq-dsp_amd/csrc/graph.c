@@ -690,6 +690,10 @@ static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
      * automatic choice). */
     const char *dk = getenv("UQ_DW");
     d->dwk = !dk ? -1 : !strcmp(dk, "band") ? 0 : !strcmp(dk, "mfma") ? 1 : !strcmp(dk, "win") ? 2 : -1;
+    /* UQ_DW_ROWS=n at load time: at most n output rows per block of the
+     * matrix-core window depthwise (0 or unset: its own choice). */
+    const char *dr = getenv("UQ_DW_ROWS");
+    d->dw_rows = dr && atoi(dr) > 0 ? atoi(dr) : 0;
     if (o->code == 15) uqk_dw_band_prepare(d);
     d->hi_shift = o->code == 14 || d->dwwin;
     for (int c = 0; c < oc; c++)

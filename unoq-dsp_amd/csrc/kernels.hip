@@ -1818,9 +1818,25 @@ __global__ __launch_bounds__(256) void k_dw_mfma(DwMArgs a)
     }
 }
 
-// Geometry of k_dw_mfma; returns its dynamic LDS bytes, 0 if the layer does
-// not suit it (then the dot4 window kernel runs it).
-static size_t dw_mfma_plan(const UQKSpatial *d, DwMArgs *t)
+// Blocks of k_dw_mfma below which a launch splits its maps into more bands
+// (four per compute unit of MI355X's 256).
+constexpr long DWM_BLOCKS = 1024;
+
+// Channel groups per block for a band of `band` output rows: enough tiles per
+// wave on small maps (a 7x7 image has four), a whole number of blocks per
+// image, the planes within 40 KiB.
+static int dw_mfma_lgb(const UQKSpatial *d, int band, int rows_p, int cols_p)
+{
+    const int tiles = (band * d->ow + 15) / 16, groups = d->oc / 16;
+    int lgb = tiles <= 4 ? 2 : tiles <= 16 ? 1 : 0;
+    while (lgb && (groups % (1 << lgb) || ((size_t)rows_p * cols_p * 16 << lgb) > 40960)) lgb--;
+    return lgb;
+}
+
+// Geometry of k_dw_mfma for a launch of `batches` images (0: only whether
+// and how the layer fits); returns its dynamic LDS bytes, 0 if the layer
+// does not suit it (then the dot4 window kernel runs it).
+static size_t dw_mfma_plan(const UQKSpatial *d, DwMArgs *t, uint32_t batches)
 {
     const int ks = d->kh, s = d->sh;
     if (!d->dwwin || d->oc % 16 || d->ic != d->oc || d->kh != d->kw || (ks != 3 && ks != 5) || d->sh != d->sw ||
@@ -1828,19 +1844,38 @@ static size_t dw_mfma_plan(const UQKSpatial *d, DwMArgs *t)
         return 0;
     t->cols_p = (d->ow - 1) * s + ks;
     // Output rows per block: the whole map when its padded window fits 40
-    // KiB, else the most rows whose window does (bands of the map).
+    // KiB, else the most rows whose window does (bands of the map). A launch
+    // of fewer than DWM_BLOCKS blocks takes more, equal bands instead, as
+    // many as it needs to reach DWM_BLOCKS while a band stages at most 1.25x
+    // its rows' share of the input. Kernel time at batch 64: 56x56x96 5x5 s2
+    // 13.4 us in bands of 20 and 8 rows (768 blocks), 11.8 in bands of 10;
+    // 112x112x32 3x3 s1 19.4 us in bands of 20 (and 12, 768 blocks), 18.4-19.3
+    // in eight of 14; a MobileNetV4-S step (launches of 2304 or more blocks)
+    // 0.4240 ms with its 5x5 s2 layer in bands of 20 and 8 rows, 0.4252 in
+    // equal bands of 14.
     const size_t row_bytes = (size_t)t->cols_p * 16;
     int band = d->oh;
     if ((size_t)((band - 1) * s + ks) * row_bytes > 40960) band = (int)((40960 / row_bytes - ks) / s + 1);
     if (band < 1 || (size_t)ks * row_bytes > 40960) return 0;
+    const auto blocks_of = [&](int b, int nb) {
+        return (long)batches * nb * ((d->oc / 16) >> dw_mfma_lgb(d, b, (b - 1) * s + ks, t->cols_p));
+    };
+    if (d->dw_rows > 0) {
+        if (band > d->dw_rows) band = d->dw_rows;
+    } else if (batches && blocks_of(band, (d->oh + band - 1) / band) < DWM_BLOCKS) {
+        int nb = (d->oh + band - 1) / band;
+        band = (d->oh + nb - 1) / nb;
+        while (band > 1 && blocks_of(band, nb) < DWM_BLOCKS) {
+            const int nb2 = nb + 1, band2 = (d->oh + nb2 - 1) / nb2;
+            if (((band2 - 1) * s + ks) * 4 > band2 * s * 5) break;
+            nb = nb2;
+            band = band2;
+        }
+    }
     t->band = band;
     t->bands = (d->oh + band - 1) / band;
     t->rows_p = (band - 1) * s + ks;
-    // Groups per block: enough tiles per wave on small maps (a 7x7 image has
-    // four), a whole number of blocks per image, the planes within 40 KiB.
-    const int tiles = (band * d->ow + 15) / 16, groups = d->oc / 16;
-    int lgb = tiles <= 4 ? 2 : tiles <= 16 ? 1 : 0;
-    while (lgb && (groups % (1 << lgb) || ((size_t)t->rows_p * t->cols_p * 16 << lgb) > 40960)) lgb--;
+    const int lgb = dw_mfma_lgb(d, band, t->rows_p, t->cols_p);
     t->lgb = lgb;
     t->lwg = 2 - lgb;
     const size_t bytes = (size_t)t->rows_p * t->cols_p * 16 << lgb;
@@ -1853,7 +1888,7 @@ static size_t dw_mfma_plan(const UQKSpatial *d, DwMArgs *t)
 static int launch_dw_mfma(const UQKSpatial *d, const void *x, void *y, uint32_t batches)
 {
     DwMArgs a;
-    const size_t lds = dw_mfma_plan(d, &a);
+    const size_t lds = dw_mfma_plan(d, &a, batches);
     if (!lds) return -1;
     a.x = (const int8_t *)x;
     a.y = (int8_t *)y;
@@ -1975,7 +2010,7 @@ extern "C" int uqk_depthwise(const UQKSpatial *d, const void *x, void *y, uint32
         if (d->dwb[0] > 0 && (d->dwk == 0 || (d->dwk < 0 && d->kh == 3 && d->sh == 2)))
             return uqk_dw_band(d, x, y, batches);
         DwMArgs t;
-        if (d->dwk != 2 && dw_mfma_plan(d, &t)) return launch_dw_mfma(d, x, y, batches) < 0 ? (int)hipErrorInvalidValue : 0;
+        if (d->dwk != 2 && dw_mfma_plan(d, &t, 0)) return launch_dw_mfma(d, x, y, batches) < 0 ? (int)hipErrorInvalidValue : 0;
         return launch_dw_win(d, x, y, batches) < 0 ? (int)hipErrorInvalidValue : 0;
     }
     const int rc = launch_dw_tile(d, x, y, batches);
