@@ -124,10 +124,12 @@ def test_gemm_rows_plans(lib, seed, monkeypatch):
 
 @pytest.mark.parametrize("seed", range(48))
 def test_gemm_plans(lib, seed, monkeypatch):
-    """Convs forced onto the large-tile GEMM (all four tile configurations) with pixel,
-    channel and K tails, compared in full with the oracle."""
+    """Convs forced onto the large-tile GEMM (all four tile configurations,
+    one or two output tiles per block) with pixel, channel and K tails,
+    compared in full with the oracle."""
     monkeypatch.setenv("UQ_GEMM", "1")
     monkeypatch.setenv("UQ_GEMM_TILE", str(seed % 4))
+    monkeypatch.setenv("UQ_GEMM_TPB", str(1 + (seed // 4) % 2))
     plan = gemm_plan(9000 + seed)
     images = 2 + seed % 3
     x = P.random_input(plan, images, seed)

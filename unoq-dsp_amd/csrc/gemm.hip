@@ -52,7 +52,8 @@ struct GemmArgs {
     int K, kpad, oc, oc_pad;
     int ih, iw, ic, ow, ohw, kw, sh, sw, dh, dw, pt, pl;
     int xz, yz, lo, hi;
-    int ctiles, nblocks;
+    int ctiles, nblocks;       // channel tiles; blocks launched
+    int ntiles;                // output tiles of the launch
     int rotate;                // start each block's K walk at a different stage
 };
 
@@ -150,7 +151,13 @@ __device__ __forceinline__ void gemm_store(const v16i (&acc)[CT][PT], const EpiL
 // tap); otherwise pointwise rows of IC bytes. NS: stages in the LDS ring;
 // KS: K bytes per stage (64, or 128 so that every staged row is one whole
 // 128-byte line, which halves the L2 requests per byte).
-template <int WP, int WC, int NWP, int NWC, int NS, int KS, bool IM2COL, int EMODE>
+//
+// TPB: output tiles per block. With TPB = 2 a block takes tiles 2b and 2b + 1
+// (b its XCD-aware rank): once the first tile's last stage has been read,
+// the second tile's first stage is issued before the first tile's epilogue,
+// so that its latency and the block's start-up (records, address set-up)
+// are paid once per two tiles.
+template <int WP, int WC, int NWP, int NWC, int NS, int KS, bool IM2COL, int EMODE, int TPB>
 __global__ __launch_bounds__(64 * NWP * NWC) void k_gemm(GemmArgs a)
 {
     constexpr int NW = NWP * NWC, T = 64 * NW;
@@ -165,19 +172,23 @@ __global__ __launch_bounds__(64 * NWP * NWC) void k_gemm(GemmArgs a)
     static_assert(NS >= 2 && NS <= 6 && (NS - 1) * NI < 64, "stage ring");
 
     __shared__ __attribute__((aligned(1024))) int8_t ring[NS * STAGE];
-    __shared__ __attribute__((aligned(16))) int r_m[BC], r_t[BC], r_b[BC], r_ls[BC];
-    __shared__ __attribute__((aligned(16))) long long r_c1[BC], r_thr[BC];
+    __shared__ __attribute__((aligned(16))) int r_m[TPB][BC], r_t[TPB][BC], r_b[TPB][BC], r_ls[TPB][BC];
+    __shared__ __attribute__((aligned(16))) long long r_c1[TPB][BC], r_thr[TPB][BC];
     __shared__ __attribute__((aligned(16))) int8_t lut_s[256];
 
     const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int wp = wave % NWP, wc = wave / NWP;
     const int nb = a.nblocks, q8 = nb >> 3, r8 = nb & 7, xcd = (int)(blockIdx.x & 7);
-    const int lid = xcd * q8 + min(xcd, r8) + (int)(blockIdx.x >> 3);
-    const int p0 = lid / a.ctiles * BP, c0 = lid % a.ctiles * BC;
+    const int bid = xcd * q8 + min(xcd, r8) + (int)(blockIdx.x >> 3);
+    // This block's tiles: bid * TPB + j for j < ntile.
+    const int ntile = min(TPB, a.ntiles - bid * TPB);
 
-    const EpiLds recs = {r_m, r_t, r_b, r_ls, r_c1, r_thr};
-    load_records<T>(recs, a.epi, c0, BC, a.oc, t);
+    auto recs = [&](int j) { return EpiLds{r_m[j], r_t[j], r_b[j], r_ls[j], r_c1[j], r_thr[j]}; };
+#pragma unroll
+    for (int j = 0; j < TPB; j++)
+        if (j < ntile) load_records<T>(recs(j), a.epi, (bid * TPB + j) % a.ctiles * BC, BC, a.oc, t);
     if (a.lut && t < 64) ((int *)lut_s)[t] = ((const int *)a.lut)[t];
+    int lid = bid * TPB, p0 = 0, c0 = 0;
 
     // Staging: a stage is BP pixel rows then BC weight rows of KS bytes.
     // Wave w's instruction i fills stage bytes [j * 1024, j * 1024 + 1024)
@@ -191,30 +202,38 @@ __global__ __launch_bounds__(64 * NWP * NWC) void k_gemm(GemmArgs a)
     const int8_t *pad = (const int8_t *)g_pad_rows.b + (a.xz & 0xff) * 16, *zero = (const int8_t *)g_pad_rows.b;
     const int8_t *xsrc[NIX];
     int iy0[NIX], ix0[NIX];
-#pragma unroll
-    for (int i = 0; i < NIX; i++) {
-        const int p = min(p0 + (wave + i * NW) * RPI + lane / CPR, a.M - 1);
-        if (IM2COL) {
-            const int n = p / a.ohw, rem = p - n * a.ohw, oy = rem / a.ow, ox = rem - oy * a.ow;
-            iy0[i] = oy * a.sh - a.pt;
-            ix0[i] = ox * a.sw - a.pl;
-            xsrc[i] = a.x + (long)n * a.ih * a.iw * a.ic + ((long)iy0[i] * a.iw + ix0[i]) * a.ic + cq * 16;
-        } else {
-            iy0[i] = ix0[i] = 0;
-            xsrc[i] = a.x + (long)p * a.ic + cq * 16;
-        }
-    }
     const int8_t *wsrc[NIW];
-#pragma unroll
-    for (int i = 0; i < NIW; i++)
-        wsrc[i] = a.w + (long)min(c0 + (wave + (NIX + i) * NW) * RPI - BP + lane / CPR, a.oc_pad - 1) * a.kpad + cq * 16;
-
     // The block's walk over the S stages of K starts at stage `rot` (the sum
     // does not depend on the order): blocks that run side by side then read
     // different weight and pixel lines at any one time instead of all
     // requesting the same lines of L2 together.
     const int S = (a.kpad + KS - 1) / KS;
-    const int rot = a.rotate ? lid % S : 0;
+    int rot = 0;
+    // Tile `tile`'s origin and its staging sources.
+    auto setup = [&](int tile) {
+        lid = tile;
+        p0 = lid / a.ctiles * BP;
+        c0 = lid % a.ctiles * BC;
+        rot = a.rotate ? lid % S : 0;
+#pragma unroll
+        for (int i = 0; i < NIX; i++) {
+            const int p = min(p0 + (wave + i * NW) * RPI + lane / CPR, a.M - 1);
+            if (IM2COL) {
+                const int n = p / a.ohw, rem = p - n * a.ohw, oy = rem / a.ow, ox = rem - oy * a.ow;
+                iy0[i] = oy * a.sh - a.pt;
+                ix0[i] = ox * a.sw - a.pl;
+                xsrc[i] = a.x + (long)n * a.ih * a.iw * a.ic + ((long)iy0[i] * a.iw + ix0[i]) * a.ic + cq * 16;
+            } else {
+                iy0[i] = ix0[i] = 0;
+                xsrc[i] = a.x + (long)p * a.ic + cq * 16;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NIW; i++)
+            wsrc[i] = a.w + (long)min(c0 + (wave + (NIX + i) * NW) * RPI - BP + lane / CPR, a.oc_pad - 1) * a.kpad +
+                      cq * 16;
+    };
+    setup(bid * TPB);
     const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t *)ring;
     auto issue = [&](int s, int buf) {
         const int ks = s + rot < S ? s + rot : s + rot - S;
@@ -244,12 +263,6 @@ __global__ __launch_bounds__(64 * NWP * NWC) void k_gemm(GemmArgs a)
     };
 
     v16i acc[CT][PT];
-#pragma unroll
-    for (int ct = 0; ct < CT; ct++)
-#pragma unroll
-        for (int pt = 0; pt < PT; pt++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[ct][pt][r] = 0;
 
     // Fragments of one 32-byte K half of a staged stage: lane (fr, fh)
     // takes logical chunk 2h + fh of weight row wc*WC + ct*32 + fr and of
@@ -300,6 +313,13 @@ __global__ __launch_bounds__(64 * NWP * NWC) void k_gemm(GemmArgs a)
 #pragma unroll
     for (int s = 0; s < NS; s++)
         if (s < S) issue(s, s);
+    for (int j = 0;;) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+        for (int pt = 0; pt < PT; pt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[ct][pt][r] = 0;
     wait_stage(min(NS - 1, S - 1));
     __syncthreads();
     v4i wf[2][CT], xf[2][PT];
@@ -335,8 +355,22 @@ __global__ __launch_bounds__(64 * NWP * NWC) void k_gemm(GemmArgs a)
         mfmas(wf[h & 1], xf[h & 1]);
     }
 
-    gemm_store<PT, CT, HI, CORR>(acc, recs, lut_s, a.lut != nullptr, a.y, a.oc, a.yz, a.lo, a.hi, wc * WC,
-                                 c0 + wc * WC, (long)p0 + wp * WP, a.M, lane);
+    // The next tile's first stage goes in before this tile's epilogue (after
+    // a barrier: every wave has read the ring), its other stages after it.
+    const int cp0 = p0, cc0 = c0, cur = j;
+    const bool more = ++j < ntile;
+    if (more) {
+        __syncthreads();
+        setup(bid * TPB + j);
+        issue(0, 0);
+    }
+    gemm_store<PT, CT, HI, CORR>(acc, recs(cur), lut_s, a.lut != nullptr, a.y, a.oc, a.yz, a.lo, a.hi, wc * WC,
+                                 cc0 + wc * WC, (long)cp0 + wp * WP, a.M, lane);
+    if (!more) break;
+#pragma unroll
+    for (int s = 1; s < NS; s++)
+        if (s < S) issue(s, s);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -548,24 +582,52 @@ __global__ __launch_bounds__(64 * RG_NW) void k_gemm_rows(RowsArgs a)
 }
 
 static uint64_t g_launches;     // successful launches, for tests that must know which kernel ran
+static int g_cus;               // compute units of the device (persistent grid sizes)
+
+// Sets g_cus on first use; nonzero if the device cannot be queried.
+static int cu_count(void)
+{
+    if (g_cus) return 0;
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n < 1)
+        return 1;
+    g_cus = n;
+    return 0;
+}
 
 // Launches of the large-tile GEMM since the library was loaded (a test hook;
 // not part of the plan ABI).
 extern "C" uint64_t uqk_gemm_launches(void) { return g_launches; }
 
+template <int WP, int WC, int NWP, int NWC, int NS, int KS, bool IM2COL, int TPB>
+static void launch_gemm_tpb(const GemmArgs &a, int emode, dim3 grid, dim3 block, hipStream_t st, hipEvent_t e0,
+                            hipEvent_t e1)
+{
+    switch (emode) {
+    case 0: hipExtLaunchKernelGGL((k_gemm<WP, WC, NWP, NWC, NS, KS, IM2COL, 0, TPB>), grid, block, 0, st, e0, e1, 0u, a); break;
+    case 1: hipExtLaunchKernelGGL((k_gemm<WP, WC, NWP, NWC, NS, KS, IM2COL, 1, TPB>), grid, block, 0, st, e0, e1, 0u, a); break;
+    case 2: hipExtLaunchKernelGGL((k_gemm<WP, WC, NWP, NWC, NS, KS, IM2COL, 2, TPB>), grid, block, 0, st, e0, e1, 0u, a); break;
+    default: hipExtLaunchKernelGGL((k_gemm<WP, WC, NWP, NWC, NS, KS, IM2COL, 3, TPB>), grid, block, 0, st, e0, e1, 0u, a); break;
+    }
+}
+
+// Two tiles per block when the launch has more tiles than the device has
+// compute units (more than one round of blocks) and a block fills its
+// compute unit (eight waves), else one: the four-wave configuration relies
+// on two blocks per compute unit, whose LDS the second record buffer would
+// no longer fit.
 template <int WP, int WC, int NWP, int NWC, int NS, int KS, bool IM2COL>
-static int launch_gemm(const GemmArgs &a, int emode)
+static int launch_gemm(GemmArgs a, int emode, int tpb_forced)
 {
     hipStream_t st;
     hipEvent_t e0, e1;
     uqk_next_launch(&st, &e0, &e1);
+    const int tpb = tpb_forced == 1 || tpb_forced == 2 ? tpb_forced : a.ntiles > g_cus && NWP * NWC == 8 ? 2 : 1;
+    a.nblocks = (a.ntiles + tpb - 1) / tpb;
     const dim3 grid((unsigned)a.nblocks), block(64 * NWP * NWC);
-    switch (emode) {
-    case 0: hipExtLaunchKernelGGL((k_gemm<WP, WC, NWP, NWC, NS, KS, IM2COL, 0>), grid, block, 0, st, e0, e1, 0u, a); break;
-    case 1: hipExtLaunchKernelGGL((k_gemm<WP, WC, NWP, NWC, NS, KS, IM2COL, 1>), grid, block, 0, st, e0, e1, 0u, a); break;
-    case 2: hipExtLaunchKernelGGL((k_gemm<WP, WC, NWP, NWC, NS, KS, IM2COL, 2>), grid, block, 0, st, e0, e1, 0u, a); break;
-    default: hipExtLaunchKernelGGL((k_gemm<WP, WC, NWP, NWC, NS, KS, IM2COL, 3>), grid, block, 0, st, e0, e1, 0u, a); break;
-    }
+    if (tpb == 2) launch_gemm_tpb<WP, WC, NWP, NWC, NS, KS, IM2COL, 2>(a, emode, grid, block, st, e0, e1);
+    else launch_gemm_tpb<WP, WC, NWP, NWC, NS, KS, IM2COL, 1>(a, emode, grid, block, st, e0, e1);
     const int rc = uqk_fail(hipGetLastError());
     if (!rc) g_launches++;
     return rc;
@@ -582,13 +644,13 @@ static const int g_tile_ks[4] = {64, 64, 128, 128};
 static const int g_tile_bc[4] = {128, 256, 128, 256};
 
 template <bool IM2COL>
-static int launch_tile(int tile, const GemmArgs &a, int emode)
+static int launch_tile(int tile, const GemmArgs &a, int emode, int tpb)
 {
     switch (tile) {
-    case 1: return launch_gemm<128, 64, 2, 4, 3, 64, IM2COL>(a, emode);
-    case 2: return launch_gemm<64, 64, 4, 2, 3, 128, IM2COL>(a, emode);
-    case 3: return launch_gemm<128, 64, 2, 4, 2, 128, IM2COL>(a, emode);
-    default: return launch_gemm<128, 64, 2, 2, 3, 64, IM2COL>(a, emode);
+    case 1: return launch_gemm<128, 64, 2, 4, 3, 64, IM2COL>(a, emode, tpb);
+    case 2: return launch_gemm<64, 64, 4, 2, 3, 128, IM2COL>(a, emode, tpb);
+    case 3: return launch_gemm<128, 64, 2, 4, 2, 128, IM2COL>(a, emode, tpb);
+    default: return launch_gemm<128, 64, 2, 2, 3, 64, IM2COL>(a, emode, tpb);
     }
 }
 
@@ -611,17 +673,10 @@ static int rows_fit(const UQKSpatial *d, int *cols)
     return 1;
 }
 
-static int g_cus;               // compute units of the device (persistent grid size)
 
 static int launch_rows(const UQKSpatial *d, const void *x, void *y, uint32_t batches, int cols, int emode)
 {
-    if (!g_cus) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            n < 1)
-            return uqk_fail(hipErrorInvalidDevice);
-        g_cus = n;
-    }
+    if (cu_count()) return uqk_fail(hipErrorInvalidDevice);
     RowsArgs a;
     a.x = (const int8_t *)x;
     a.y = (int8_t *)y;
@@ -710,10 +765,12 @@ extern "C" int uqk_gemm(const UQKSpatial *d, const void *x, void *y, uint32_t ba
     }
     const int bp = 256, bc = g_tile_bc[tile];
     a.ctiles = (d->oc + bc - 1) / bc;
-    const uint64_t blocks = (pixels + bp - 1) / bp * (uint64_t)a.ctiles;
-    if (blocks > 0x7fffffffULL) return (int)hipErrorInvalidValue;
-    a.nblocks = (int)blocks;
-    return d->mode != UQK_PW ? launch_tile<true>(tile, a, emode) : launch_tile<false>(tile, a, emode);
+    const uint64_t tiles = (pixels + bp - 1) / bp * (uint64_t)a.ctiles;
+    if (tiles > 0x7fffffffULL) return (int)hipErrorInvalidValue;
+    a.ntiles = (int)tiles;
+    if (cu_count()) return uqk_fail(hipErrorInvalidDevice);
+    return d->mode != UQK_PW ? launch_tile<true>(tile, a, emode, d->gemm_tpb)
+                             : launch_tile<false>(tile, a, emode, d->gemm_tpb);
 }
 
 // ---------------------------------------------------------------------------
@@ -766,13 +823,7 @@ __global__ __launch_bounds__(256) void k_mfma_ceiling(int iters)
 extern "C" int uqk_mfma_ceiling(int iters, int warmup, int reps, double *tops, double *us)
 {
     if (iters < 1 || reps < 1 || warmup < 0 || !tops || !us) return (int)hipErrorInvalidValue;
-    if (!g_cus) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            n < 1)
-            return uqk_fail(hipErrorInvalidDevice);
-        g_cus = n;
-    }
+    if (cu_count()) return uqk_fail(hipErrorInvalidDevice);
     hipStream_t st;
     hipEvent_t e0, e1;
     uqk_next_launch(&st, &e0, &e1);

@@ -681,11 +681,14 @@ static void prepare_spatial(uint32_t i, const Layout *L, uint8_t *host_pool)
     const int oc = q[17];
     const int32_t *bias = q + UQ_HEAD, *mult = bias + oc, *shift = mult + oc;
     d->dwwin = o->code == 15 && uqk_dw_win_lds(d) > 0;
-    /* Large-tile GEMM policy (UQ_GEMM=0/1 and UQ_GEMM_TILE=0..4 at load
-     * time override the automatic choice). */
+    /* Large-tile GEMM policy (UQ_GEMM=0/1, UQ_GEMM_TILE=0..4 and
+     * UQ_GEMM_TPB=1/2, tiles per block, at load time override the automatic
+     * choice). */
     const char *ge = getenv("UQ_GEMM"), *gt = getenv("UQ_GEMM_TILE");
     d->gemm = ge && (!strcmp(ge, "0") || !strcmp(ge, "1")) ? atoi(ge) : -1;
     d->gemm_tile = gt && gt[0] >= '0' && gt[0] <= '4' && !gt[1] ? gt[0] - '0' : -1;
+    const char *gp = getenv("UQ_GEMM_TPB");
+    d->gemm_tpb = gp && (!strcmp(gp, "1") || !strcmp(gp, "2")) ? gp[0] - '0' : 0;
     /* Depthwise kernel (UQ_DW=band, mfma or win at load time overrides the
      * automatic choice). */
     const char *dk = getenv("UQ_DW");

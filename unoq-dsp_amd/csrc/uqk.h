@@ -31,6 +31,7 @@ typedef struct {
     int32_t dwwin;             /* depthwise on tap windows (k_dw_win); wdot holds [ky][wk][C] tap words */
     int32_t gemm;              /* large-tile GEMM: -1 when the launch is large enough, 0 never, 1 whenever the shape fits */
     int32_t gemm_tile;         /* its tile configuration: -1 automatic, else 0..4 (gemm.hip) */
+    int32_t gemm_tpb;          /* its output tiles per block: 0 automatic, else 1 or 2 */
     int32_t dwk;               /* depthwise kernel: -1 automatic, 0 band (dw.hip), 1 matrix-core window, 2 dot4 window */
     int32_t dw_rows;           /* matrix-core window depthwise: most output rows per block (0: automatic) */
     int32_t dwb[4];            /* band depthwise plan (uqk_dw_band_prepare): channel groups per block (0: the layer
