@@ -259,6 +259,31 @@ def pointwise_wide_plan(seed):
     return p.build(y)
 
 
+def conv_mean_plan(seed):
+    """A 1x1 conv followed by the global mean over its output (the classifier
+    head the fused conv + mean kernel takes): maps of 1 to 64 pixels, input
+    channels 32-256, output channels multiples of 32, post tables,
+    activations, all requantisation ranges, the mean's own scale and zero
+    point; sometimes an op after the mean, sometimes a second reader of the
+    conv's output (then nothing is fused)."""
+    rng = Rng(seed, 454545)
+    p = Plan(seed)
+    h, w = _pick(rng, [(7, 7), (1, 1), (8, 8), (4, 9), (3, 5), (2, 2), (7, 9)])
+    x = p.input((1, h, w, int(_pick(rng, [32, 64, 96, 128, 256]))), zp=int(rng.integers(1, -128, 127)[0]))
+    lo = int(rng.integers(1, -24, -1)[0])
+    shift = _pick(rng, [(lo, 3), (-12, -4), (-20, -1)])
+    y = p.conv(x, _pick(rng, [32, 64, 96, 160, 320, 960]), k=1, act=_pick(rng, ["none", "relu", "relu6"]),
+               q6=int(rng.integers(1, 1, 200)[0]), lut=_random_lut(p, rng) if _pick(rng, [0, 1]) else None,
+               shift=shift, w_sigma=_pick(rng, [3, 40, 90]))
+    m = p.mean(y, scale_ratio=float(_pick(rng, [1.0, 0.37, 2.5])), yz=int(rng.integers(1, -20, 20)[0]))
+    if _pick(rng, [0, 0, 1]):
+        m = p.conv(m, 32, k=1, act="none", shift=(-12, -4))
+    if _pick(rng, [0, 0, 0, 1]):
+        # A second reader of the conv's output: the pair is not fused.
+        m = p.concat(m, p.mean(y), axis=3)
+    return p.build(m)
+
+
 def conv_add_bytes_plan(seed):
     """As conv_add_plan with channel counts that are not multiples of 16 (the
     epilogue's byte path)."""

@@ -12,9 +12,9 @@ import pytest
 
 import uq_plan as P
 import uq_workloads as W
-from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, dw_band_plan, dw_mfma_plan,
-                       gemm_plan, gemm_rows_plan, ib_plan, random_plan, pointwise_wide_plan, rows_conv_plan, stem_conv_plan,
-                       stem_plan, uib_block)
+from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, conv_mean_plan, dw_band_plan,
+                       dw_mfma_plan, gemm_plan, gemm_rows_plan, ib_plan, random_plan, pointwise_wide_plan,
+                       rows_conv_plan, stem_conv_plan, stem_plan, uib_block)
 from test_oracle_vs_reference import (BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, softmax_table_plan,
                                       transpose_plan)
 from refs import oracle_run
@@ -401,6 +401,33 @@ def test_stem_conv_fusion(lib, monkeypatch, seed):
     before = lib.uqk_stem_conv_launches()
     _assert_same(Graph(plan, lib).run_batch(x, images), want, f"unfused stem plan {seed}")
     assert lib.uqk_stem_conv_launches() == before
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_conv_mean_fusion(lib, monkeypatch, seed):
+    """A 1x1 conv and the global mean over its output run as one launch
+    (head.hip) unless the conv's output has a second reader: one to three
+    images match the oracle byte for byte, as they do unfused
+    (UQ_FUSE_MEAN=0); after a host-buffer run a snapshot of the conv's output
+    is rebuilt."""
+    plan = conv_mean_plan(seed)
+    images = 1 + seed % 3
+    x = P.random_input(plan, images, seed)
+    want = _oracle(plan, x, images)
+    ops = P.op_records(plan)
+    conv_out = ops[0][3]
+    fused = sum(1 for o in ops if conv_out in (o[1], o[2])) == 1
+    g = Graph(plan, lib)
+    before = lib.uqk_conv_mean_launches()
+    _assert_same(g.run_batch(x, images), want, f"conv+mean plan {seed}")
+    assert (lib.uqk_conv_mean_launches() > before) == fused
+    nbytes = images * P.tensor_records(plan)[conv_out][1]
+    _, snap = oracle_run(plan, x, images, P.output_bytes(plan), snap=conv_out, snap_bytes=nbytes)
+    _assert_same(g.snapshot_images(conv_out, nbytes), snap, f"conv+mean plan {seed}: conv output snapshot")
+    monkeypatch.setenv("UQ_FUSE_MEAN", "0")
+    before = lib.uqk_conv_mean_launches()
+    _assert_same(Graph(plan, lib).run_batch(x, images), want, f"unfused conv+mean plan {seed}")
+    assert lib.uqk_conv_mean_launches() == before
 
 
 @pytest.mark.parametrize("seed", range(40))

@@ -34,12 +34,14 @@ typedef struct { uint32_t code, a, b, out, p[4]; } Op;
 /* A fused group (see find_groups): an inverted bottleneck run by one launch
  * (kind 0), a conv whose residual add runs in its epilogue (kind 1), a stem
  * conv, the 3x3 stride-2 conv over its output and optionally the 1x1 after
- * that (kind 2), or a banded universal inverted bottleneck (kind 3). */
+ * that (kind 2), a banded universal inverted bottleneck (kind 3), or a 1x1
+ * conv and the mean over its whole output (kind 4). */
 typedef struct {
     int kind;
     UQKIb desc;
     UQKUib ub;                       /* kind 3 */
     UQKAdd add;                      /* kind 1; add.res is set per launch */
+    UQKMean mean;                    /* kind 4 */
     uint32_t res;                    /* kind 1: tensor of the add's other operand */
     uint32_t first, nops, in, out;
     const uint8_t *last_in;          /* input pointer of the last fused launch */
@@ -847,6 +849,32 @@ static int find_conv_add(uint32_t i, const uint16_t *users)
     return 1;
 }
 
+/* A 1x1 conv whose output, used by nothing else, is averaged over the whole
+ * map by the next op (MobileNet's classifier head) and that fits head.hip.
+ * On unless UQ_FUSE_MEAN=0 at load time. */
+static int find_conv_mean(uint32_t i, const uint16_t *users)
+{
+    const Op *c = G.ops + i, *mn = G.ops + i + 1;
+    if (c->code != 14 || mn->code != 24 || mn->a != c->out || !uqk_conv_mean_ok(G.sp + i)) return 0;
+    const uint32_t t = c->out;
+    if (users[t] != 1 || t == G.h.output || G.ts[t].rank != 4 || G.ts[t].d[0] != 1) return 0;
+    const int32_t *q = (const int32_t *)(G.arena + G.ts[mn->b].offset);
+    if (q[0] != G.sp[i].oh * G.sp[i].ow || (int)G.ts[t].d[3] != G.sp[i].oc) return 0;
+    if (G.ts[mn->out].bytes != (uint32_t)G.sp[i].oc) return 0;
+    Group *g = &G.groups[G.ngroups];
+    memset(g, 0, sizeof *g);
+    g->kind = 4;
+    g->mean.xz = q[1]; g->mean.yz = q[2]; g->mean.m = q[3]; g->mean.s = q[4];
+    g->first = i;
+    g->nops = 2;
+    g->in = c->a;
+    g->out = mn->out;
+    G.fuse_at[i] = (uint16_t)(G.ngroups + 1);
+    G.fuse_of_tensor[t] = (uint16_t)(G.ngroups + 1);
+    G.ngroups++;
+    return 1;
+}
+
 static uint32_t find_bottleneck(uint32_t i, const uint16_t *users)
 {
     if (i + 2 >= G.h.no) return 0;
@@ -1037,6 +1065,8 @@ static void find_groups(void)
     const int bottleneck = !(env && !strcmp(env, "0"));
     const char *senv = getenv("UQ_FUSE_STEM");
     const int stem = !(senv && !strcmp(senv, "0")), stem_pw = !(senv && !strcmp(senv, "2"));
+    const char *menv = getenv("UQ_FUSE_MEAN");
+    const int conv_mean = !(menv && !strcmp(menv, "0"));
     const char *uenv = getenv("UQ_FUSE_UIB");
     const int uib = !uenv ? 1 : !strcmp(uenv, "0") ? 0 : !strcmp(uenv, "2") ? 2 : 1;
     for (uint32_t i = 0; i + 1 < G.h.no; i++) {
@@ -1044,6 +1074,7 @@ static void find_groups(void)
         if (!n && uib) n = find_uib(i, users, uib);
         if (!n && bottleneck) n = find_bottleneck(i, users);
         if (!n && find_conv_add(i, users)) n = 2;
+        if (!n && conv_mean && find_conv_mean(i, users)) n = 2;
         if (n) i += n - 1;
     }
     memset(G.fwd, 0, sizeof G.fwd);
@@ -1202,6 +1233,9 @@ static int enqueue_range(uint32_t i0, uint32_t i1, uint32_t images, uint32_t *ne
                 rc = uqk_ib(&grp->desc, G.ptr[grp->in], G.ptr[grp->out], images);
             } else if (grp->kind == 3) {
                 rc = uqk_uib(&grp->ub, G.ptr[grp->in], G.ptr[grp->out], images);
+            } else if (grp->kind == 4) {
+                rc = uqk_conv_mean(G.sp + i, &grp->mean, G.ptr[grp->in], G.ptr[grp->out],
+                                   images * G.ts[G.ops[i].a].d[0]);
             } else if (grp->kind == 1) {
                 grp->add.res = G.ptr[grp->res];
                 rc = uqk_conv_add(G.sp + i, G.ptr[grp->in], G.ptr[grp->out], images * G.ts[G.ops[i].a].d[0],

@@ -208,6 +208,16 @@ typedef struct {
 /* Whether uqk_conv_add takes a layer (the k_conv kernel modes). */
 int uqk_conv_add_ok(const UQKSpatial *d);
 int uqk_conv_add(const UQKSpatial *d, const void *x, void *y, uint32_t batches, const UQKAdd *add);
+
+/* A 1x1 conv and the mean over its whole output (head.hip): y[n][c] =
+ * mean(conv(x)[n][.][c]), the mean's parameters (op 24: input and output
+ * zero points, multiplier, shift) in UQKMean. ok: whether the conv fits
+ * (pointwise, IC % 32 == 0 and <= 256, OC % 32 == 0, at most 64 pixels). */
+typedef struct {
+    int32_t xz, yz, m, s;
+} UQKMean;
+int uqk_conv_mean_ok(const UQKSpatial *d);
+int uqk_conv_mean(const UQKSpatial *d, const UQKMean *mean, const void *x, void *y, uint32_t images);
 int uqk_depthwise(const UQKSpatial *d, const void *x, void *y, uint32_t batches);
 int uqk_pool(const UQKSpatial *d, const void *x, void *y, uint32_t batches);
 int uqk_add(const void *a, const void *b, void *y, uint64_t count, const void *tables,

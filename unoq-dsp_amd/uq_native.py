@@ -66,8 +66,9 @@ def open_library(path=None):
         fn.restype = res
         fn.argtypes = args
     # Test hooks outside the plan ABI: launches of the large-tile GEMM, of the
-    # fused bottleneck kernel and of the fused stem kernel.
-    for hook in ("uqk_gemm_launches", "uqk_ib_launches", "uqk_stem_conv_launches", "uqk_uib_launches"):
+    # fused bottleneck, stem, banded bottleneck and conv + mean kernels.
+    for hook in ("uqk_gemm_launches", "uqk_ib_launches", "uqk_stem_conv_launches", "uqk_uib_launches",
+                 "uqk_conv_mean_launches"):
         getattr(lib, hook).restype = C.c_uint64
         getattr(lib, hook).argtypes = []
     # Measurement hook: the sustained int8 matrix-core rate of a register-only
