@@ -45,6 +45,7 @@ METRIC = "images/sec @ batch 256, MobileNetV4-S int8 224²; conv int8 TOPS + DW 
 HBM_PEAK = 8.0e12          # bytes/s
 INT8_PEAK = 5.0e15         # dense int8 MFMA ops/s
 RIDGE = INT8_PEAK / HBM_PEAK
+PER_OP_PASSES = 100        # least number of per-op timing passes before the warm-up steps
 REF_RELEASE = ROOT / "oracle" / "_ref" / "libuq_ref_release.so"
 
 
@@ -58,19 +59,21 @@ def time_device(lib, graph, images, steps, warmup, seed=7):
     dout = DeviceBuffer(lib, images * graph.output_bytes)
     din.upload(x)
     # Per-op durations from HIP events stamped by the kernels' own dispatches
-    # (first start to last end of each op's kernels), over the same number
-    # of passes as the timed steps. They run first: their passes also bring
-    # the GPU clock up, which otherwise keeps rising over the first few tens
-    # of passes, so that a short timed region after a few warm-up steps
-    # measures the steady state.
+    # (first start to last end of each op's kernels), averaged over at least
+    # PER_OP_PASSES passes (more when more steps are timed). They run first:
+    # their passes also bring the GPU clock up, which otherwise keeps rising
+    # over the first passes: MobileNetV4-S timed over 20 steps after 5
+    # warm-up steps measured 0.441 ms/step after 20 such passes, 0.434 after
+    # 100 with enqueued warm-up steps, against 0.421 over 200 steps after 50.
     graph.profile(1)
-    for _ in range(steps):
+    for _ in range(max(steps, PER_OP_PASSES)):
         rc = lib.ug_run_device(din.ptr, dout.ptr, images)
         assert rc == 0, rc
     counters = graph.profile(2)
     graph.profile(0)
+    # Warm-up steps exactly as the timed ones: enqueued back to back.
     for _ in range(warmup):
-        rc = lib.ug_run_device(din.ptr, dout.ptr, images)
+        rc = lib.ug_enqueue_device(din.ptr, dout.ptr, images)
         assert rc == 0, rc
     assert lib.ug_synchronize() == 0
     t0 = time.perf_counter()
