@@ -409,7 +409,8 @@ def test_conv_mean_fusion(lib, monkeypatch, seed):
     (head.hip) unless the conv's output has a second reader: one to three
     images match the oracle byte for byte, as they do unfused
     (UQ_FUSE_MEAN=0); after a host-buffer run a snapshot of the conv's output
-    is rebuilt."""
+    is rebuilt. The fused kernel's channel tiles are split over one to four
+    workgroups per image (UQ_MEAN_PARTS; more parts than tiles are capped)."""
     plan = conv_mean_plan(seed)
     images = 1 + seed % 3
     x = P.random_input(plan, images, seed)
@@ -417,6 +418,7 @@ def test_conv_mean_fusion(lib, monkeypatch, seed):
     ops = P.op_records(plan)
     conv_out = ops[0][3]
     fused = sum(1 for o in ops if conv_out in (o[1], o[2])) == 1
+    monkeypatch.setenv("UQ_MEAN_PARTS", str(1 + (seed // 3) % 4))
     g = Graph(plan, lib)
     before = lib.uqk_conv_mean_launches()
     _assert_same(g.run_batch(x, images), want, f"conv+mean plan {seed}")

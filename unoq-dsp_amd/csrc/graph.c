@@ -865,6 +865,10 @@ static int find_conv_mean(uint32_t i, const uint16_t *users)
     memset(g, 0, sizeof *g);
     g->kind = 4;
     g->mean.xz = q[1]; g->mean.yz = q[2]; g->mean.m = q[3]; g->mean.s = q[4];
+    /* UQ_MEAN_PARTS=n at load time: n workgroups per image (0 or unset:
+     * automatic). */
+    const char *pe = getenv("UQ_MEAN_PARTS");
+    g->mean.parts = pe && atoi(pe) > 0 && atoi(pe) <= 8 ? atoi(pe) : 0;
     g->first = i;
     g->nops = 2;
     g->in = c->a;

@@ -2,9 +2,10 @@
 // classifier head of MobileNet-style networks (code 14, 1x1 stride 1, then
 // code 24 over the whole map; the reference runs them one after the other
 // through its arena: qnn.c:1101-1169 / gemm.c:592-612 for the conv,
-// qnn.c:184-198 for the mean). The conv's output is never written: one
-// workgroup per image keeps the image's P <= 64 pixels of input in LDS,
-// computes every output channel on the matrix cores, requantises each value
+// qnn.c:184-198 for the mean). The conv's output is never written: each of
+// an image's workgroups (two by default, each a contiguous share of the
+// output channels) keeps the image's P <= 64 pixels of input in LDS,
+// computes its output channels on the matrix cores, requantises each value
 // exactly as the conv kernels do (its records, clamp and post table), and
 // sums the int8 results of each channel over the image's pixels; the mean's
 // own requantisation (uq_scale, zero points, clamp, as k_mean) then gives
@@ -30,6 +31,11 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 constexpr int HM_WAVES = 8;            // waves per workgroup
 constexpr int HM_MAXK = 8;             // K steps of 32 bytes: IC <= 256
 constexpr int HM_MAXP = 64;            // pixels per image
+// Workgroups per image by default. MobileNetV4-S's 960 channels (30 tiles of
+// 32) in two parts leave each wave one or two tiles instead of three or four:
+// its step 0.4228 -> 0.4199-0.4204 ms (one, three and six parts: 0.4228,
+// 0.4220, 0.4236 ms; four: 0.4197-0.4204, with twice the input staging).
+constexpr int HM_PARTS = 2;
 
 struct HeadArgs {
     const int8_t *x;                   // [images][P][IC]
@@ -38,6 +44,7 @@ struct HeadArgs {
     const int4 *epi;                   // the conv's records, one per channel
     const uint8_t *lut;                // the conv's optional post table
     int P, IC, OC, kpad;
+    int parts;                         // workgroups per image
     int yz, lo, hi;                    // the conv's output zero point and clamp
     int m_xz, m_yz, m_m, m_s;          // the mean's input/output zero points, multiplier, shift
 };
@@ -49,7 +56,7 @@ __global__ __launch_bounds__(64 * HM_WAVES) void k_conv_mean(HeadArgs a)
     __shared__ __attribute__((aligned(16))) int8_t lut_s[256];
     const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int fr = lane & 31, fh = lane >> 5;
-    const int n = blockIdx.x;
+    const int n = blockIdx.x / a.parts, part = blockIdx.x - n * a.parts;
     const int xs = a.IC + 16;                          // LDS row stride (16-byte pad: rows on distinct banks)
 
     // The image's pixels into LDS, 16 bytes per thread and step.
@@ -62,8 +69,10 @@ __global__ __launch_bounds__(64 * HM_WAVES) void k_conv_mean(HeadArgs a)
     if (a.lut && t < 64) ((int *)lut_s)[t] = ((const int *)a.lut)[t];
     __syncthreads();
 
+    // This workgroup's channel tiles [c0, c1), a contiguous share per wave.
     const int ks = a.IC >> 5, ctiles = a.OC >> 5;
-    const int i0 = wave * ctiles / HM_WAVES, i1 = (wave + 1) * ctiles / HM_WAVES;
+    const int c0 = part * ctiles / a.parts, c1 = (part + 1) * ctiles / a.parts;
+    const int i0 = c0 + wave * (c1 - c0) / HM_WAVES, i1 = c0 + (wave + 1) * (c1 - c0) / HM_WAVES;
     const int vlo = vgpr(a.lo), vhi = vgpr(a.hi);
     // Weight fragments of tile ct (channel ct*32 + fr, K bytes 32s + 16fh)
     // and its channel's record, loaded one tile ahead.
@@ -145,10 +154,13 @@ extern "C" int uqk_conv_mean(const UQKSpatial *d, const UQKMean *mean, const voi
     a.P = d->oh * d->ow; a.IC = d->ic; a.OC = d->oc; a.kpad = d->kpad;
     a.yz = d->yz; a.lo = d->lo; a.hi = d->hi;
     a.m_xz = mean->xz; a.m_yz = mean->yz; a.m_m = mean->m; a.m_s = mean->s;
+    a.parts = mean->parts > 0 ? mean->parts : HM_PARTS;
+    if (a.parts > (a.OC >> 5)) a.parts = a.OC >> 5;
+    if ((unsigned long long)images * a.parts > 0x7fffffffULL) return (int)hipErrorInvalidValue;
     hipStream_t st;
     hipEvent_t e0, e1;
     uqk_next_launch(&st, &e0, &e1);
-    const dim3 grid(images), block(64 * HM_WAVES);
+    const dim3 grid(images * a.parts), block(64 * HM_WAVES);
     switch ((d->hi_shift ? 1 : 0) | (d->corr ? 2 : 0)) {
     case 0: hipExtLaunchKernelGGL((k_conv_mean<false, false>), grid, block, 0, st, e0, e1, 0u, a); break;
     case 1: hipExtLaunchKernelGGL((k_conv_mean<true, false>), grid, block, 0, st, e0, e1, 0u, a); break;

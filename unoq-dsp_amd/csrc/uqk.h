@@ -215,6 +215,7 @@ int uqk_conv_add(const UQKSpatial *d, const void *x, void *y, uint32_t batches, 
  * (pointwise, IC % 32 == 0 and <= 256, OC % 32 == 0, at most 64 pixels). */
 typedef struct {
     int32_t xz, yz, m, s;
+    int32_t parts;             /* workgroups per image, each a share of the output channels (0: automatic) */
 } UQKMean;
 int uqk_conv_mean_ok(const UQKSpatial *d);
 int uqk_conv_mean(const UQKSpatial *d, const UQKMean *mean, const void *x, void *y, uint32_t images);
