@@ -259,6 +259,38 @@ def pointwise_wide_plan(seed):
     return p.build(y)
 
 
+def gather_plan(seed):
+    """YOLO's C3k2 split / table / concat chains and their variants: a conv
+    output split in two along the channels (slices of the last axis), each
+    half through its own table, the halves concatenated and that concatenated
+    with another tensor (on either side); sometimes a half has other readers
+    (its slice stays a launch), a table reads a plain tensor, the inner
+    concat is of plain tensors, or an op follows. Channel counts that leave
+    rows unaligned to 4 and 16 bytes, maps of 1x1 to 9x9."""
+    rng = Rng(seed, 919191)
+    p = Plan(seed)
+    h, w = _pick(rng, [(1, 1), (3, 5), (8, 8), (9, 7), (2, 2)])
+    x0 = p.input((1, h, w, int(_pick(rng, [8, 16, 32]))), zp=int(rng.integers(1, -128, 127)[0]))
+    c = int(_pick(rng, [2, 5, 12, 16, 32, 48, 64]))
+    x = p.conv(x0, c, k=1, act="none", shift=(-12, -4))
+    split = int(rng.integers(1, 1, c - 1)[0]) if c > 2 else 1
+    a = p.slice(x, [0, 0, 0, 0], [1, h, w, split])
+    b = p.slice(x, [0, 0, 0, split], [1, h, w, c - split])
+    shape = int(_pick(rng, [0, 0, 1, 2, 3]))
+    if shape == 1:
+        # The second half also feeds a conv whose output joins the concat.
+        m = p.conv(b, int(_pick(rng, [4, 16, 24])), k=1, act="relu", shift=(-12, -4))
+    else:
+        m = p.conv(x, int(_pick(rng, [3, 16, 32])), k=1, act="relu", shift=(-12, -4))
+    la = p.lut(a, _random_lut(p, rng))
+    lb = p.lut(b, _random_lut(p, rng)) if shape != 2 else p.copy(b)
+    inner = p.concat(la, lb, axis=3) if shape != 3 else la
+    out = p.concat(inner, m, axis=3) if _pick(rng, [0, 1]) else p.concat(m, inner, axis=3)
+    if _pick(rng, [0, 0, 1]):
+        out = p.conv(out, 16, k=1, act="none", shift=(-12, -4))
+    return p.build(out)
+
+
 def conv_mean_plan(seed):
     """A 1x1 conv followed by the global mean over its output (the classifier
     head the fused conv + mean kernel takes): maps of 1 to 64 pixels, input

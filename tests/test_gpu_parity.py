@@ -13,6 +13,7 @@ import pytest
 import uq_plan as P
 import uq_workloads as W
 from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, conv_mean_plan, dw_band_plan,
+                       gather_plan,
                        dw_mfma_plan, gemm_plan, gemm_rows_plan, ib_plan, random_plan, pointwise_wide_plan,
                        rows_conv_plan, stem_conv_plan, stem_plan, uib_block)
 from test_oracle_vs_reference import (BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, softmax_table_plan,
@@ -401,6 +402,35 @@ def test_stem_conv_fusion(lib, monkeypatch, seed):
     before = lib.uqk_stem_conv_launches()
     _assert_same(Graph(plan, lib).run_batch(x, images), want, f"unfused stem plan {seed}")
     assert lib.uqk_stem_conv_launches() == before
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_gather_fusion(lib, monkeypatch, seed):
+    """A concat whose operands are table lookups of slices (YOLO's split /
+    SiLU / concat chains and variants) runs as one row gather: 1, 2, 3 or
+    130 images (two image slices) match the oracle byte for byte, as they do
+    with the fusion off (UQ_FUSE_GATHER=0); after a host run the skipped
+    ops' outputs (slices, lookups, inner concat) are rebuilt for snapshots."""
+    plan = gather_plan(seed)
+    images = [1, 2, 3, 130][seed % 4]
+    x = P.random_input(plan, images, seed)
+    want = _oracle(plan, x, images)
+    g = Graph(plan, lib)
+    before = lib.uqk_gather_launches()
+    _assert_same(g.run_batch(x, images), want, f"gather plan {seed}, {images} images")
+    assert lib.uqk_gather_launches() > before
+    if images < 128:
+        ops, tensors = P.op_records(plan), P.tensor_records(plan)
+        output = ops[-1][3]
+        for code, a, b, t, *_ in ops:
+            if code in (20, 22, 26) and t != output:
+                nbytes = images * tensors[t][1]
+                _, snap = oracle_run(plan, x, images, P.output_bytes(plan), snap=t, snap_bytes=nbytes)
+                _assert_same(g.snapshot_images(t, nbytes), snap, f"gather plan {seed}: snapshot of tensor {t}")
+    monkeypatch.setenv("UQ_FUSE_GATHER", "0")
+    before = lib.uqk_gather_launches()
+    _assert_same(Graph(plan, lib).run_batch(x, images), want, f"gather plan {seed} unfused")
+    assert lib.uqk_gather_launches() == before
 
 
 @pytest.mark.parametrize("seed", range(40))

@@ -34,14 +34,21 @@ typedef struct { uint32_t code, a, b, out, p[4]; } Op;
 /* A fused group (see find_groups): an inverted bottleneck run by one launch
  * (kind 0), a conv whose residual add runs in its epilogue (kind 1), a stem
  * conv, the 3x3 stride-2 conv over its output and optionally the 1x1 after
- * that (kind 2), a banded universal inverted bottleneck (kind 3), or a 1x1
- * conv and the mean over its whole output (kind 4). */
+ * that (kind 2), a banded universal inverted bottleneck (kind 3), a 1x1
+ * conv and the mean over its whole output (kind 4), or a concat whose
+ * operands' table lookups, inner concats and slices run inside its launch
+ * (kind 5, find_gather). */
 typedef struct {
     int kind;
     UQKIb desc;
     UQKUib ub;                       /* kind 3 */
     UQKAdd add;                      /* kind 1; add.res is set per launch */
     UQKMean mean;                    /* kind 4 */
+    /* kind 5: segments of the output rows (source tensor, byte offset in its
+     * rows, bytes per row, table tensor or none, index flip) and the earlier
+     * ops the launch stands in for, in plan order */
+    uint32_t nseg, seg_src[4], seg_off[4], seg_width[4], seg_lut[4], seg_has_lut[4], seg_flip[4];
+    uint32_t nelide, elide[10];
     uint32_t res;                    /* kind 1: tensor of the add's other operand */
     uint32_t first, nops, in, out;
     const uint8_t *last_in;          /* input pointer of the last fused launch */
@@ -69,6 +76,7 @@ static struct {
      * for them (materialize_group). */
     uint16_t fuse_at[UG_MAX_OP];
     uint16_t fuse_of_tensor[UG_MAX_T];   /* group index + 1 of an inner tensor */
+    uint16_t elide[UG_MAX_OP];           /* group index + 1 of a gather (kind 5) that runs op i in its launch */
     uint8_t ext[UG_MAX_T];               /* G.ptr[t] is a caller buffer this run */
     /* fwd[i]: op i's output is used only by op i + 1, a reshape (code 5) to
      * the graph output; when that output is a caller buffer, op i writes
@@ -1055,11 +1063,119 @@ static int find_stem_conv(uint32_t i, const uint16_t *users, int with_pw)
     return (int)g->nops;
 }
 
+/* Row gathers (kind 5): a concat along the last axis (op 20) of int8/uint8
+ * rows whose operands are single-use table lookups (op 22), or a single-use
+ * concat along the last axis of such lookups or plain tensors; a lookup
+ * whose input is a single-use slice of the last axis only (op 26) reads the
+ * slice's source directly. One launch (uqk_gather) writes the concat's rows
+ * from the sources through the tables, in place of the lookups, the inner
+ * concat and those slices. YOLO's C3k2 blocks (split, two SiLU tables,
+ * concat, concat with the bottleneck output) drop four launches each. On
+ * unless UQ_FUSE_GATHER=0 at load time. */
+static int rows_like(const Tensor *t, const Tensor *z)
+{
+    if (t->flags || t->rank != z->rank || t->rank < 1 || t->rank > 4 || width(t->type) != 1) return 0;
+    for (uint32_t d = 0; d + 1 < t->rank; d++)
+        if (t->d[d] != z->d[d]) return 0;
+    return 1;
+}
+
+static int gather_operand(Group *g, uint32_t t, int depth, const uint16_t *users, const uint32_t *prod,
+                          const uint8_t *taken)
+{
+    const Tensor *z = G.ts + G.ops[g->first].out;
+    const uint32_t r = z->rank;
+    if (!rows_like(G.ts + t, z)) return 0;
+    const uint32_t j = prod[t] ? prod[t] - 1 : UG_MAX_OP;
+    const int inner = j < UG_MAX_OP && !taken[j] && users[t] == 1 && t != G.h.output && t != G.h.input;
+    if (inner && depth == 0 && G.ops[j].code == 20 && G.ops[j].p[0] == r - 1 && G.ops[j].a != G.ops[j].b &&
+        g->nelide < 10) {
+        const uint32_t mark = g->nseg, em = g->nelide;
+        g->elide[g->nelide++] = j;
+        if (gather_operand(g, G.ops[j].a, 1, users, prod, taken) &&
+            gather_operand(g, G.ops[j].b, 1, users, prod, taken))
+            return 1;
+        g->nseg = mark;
+        g->nelide = em;
+    }
+    if (g->nseg >= 4) return 0;
+    const uint32_t k = g->nseg;
+    g->seg_src[k] = t;
+    g->seg_off[k] = 0;
+    g->seg_width[k] = G.ts[t].d[r - 1];
+    g->seg_has_lut[k] = 0;
+    g->seg_lut[k] = g->seg_flip[k] = 0;
+    if (inner && G.ops[j].code == 22 && rows_like(G.ts + G.ops[j].a, z) && g->nelide < 10) {
+        const uint32_t s = G.ops[j].a;
+        g->elide[g->nelide++] = j;
+        g->seg_src[k] = s;
+        g->seg_width[k] = G.ts[s].d[r - 1];
+        g->seg_has_lut[k] = 1;
+        g->seg_lut[k] = G.ops[j].b;
+        g->seg_flip[k] = G.ts[s].type == 3 ? 128u : 0u;
+        /* A single-use slice of the last axis: read its source. */
+        const uint32_t i = prod[s] ? prod[s] - 1 : UG_MAX_OP;
+        if (i < UG_MAX_OP && !taken[i] && G.ops[i].code == 26 && users[s] == 1 && s != G.h.output &&
+            s != G.h.input && rows_like(G.ts + G.ops[i].a, z) && g->nelide < 10) {
+            const Tensor *x = G.ts + G.ops[i].a, *y = G.ts + s;
+            int ok = 1;
+            for (uint32_t d = 0; d + 1 < r; d++)
+                if (G.ops[i].p[d] != 0) ok = 0;
+            if (ok && (uint64_t)G.ops[i].p[r - 1] + y->d[r - 1] <= x->d[r - 1]) {
+                g->elide[g->nelide++] = i;
+                g->seg_src[k] = G.ops[i].a;
+                g->seg_off[k] = G.ops[i].p[r - 1];
+            }
+        }
+    }
+    g->nseg++;
+    return 1;
+}
+
+static int find_gather(uint32_t k, const uint16_t *users, const uint32_t *prod, uint8_t *taken)
+{
+    const Op *o = G.ops + k;
+    if (o->code != 20 || taken[k] || o->a == o->b) return 0;
+    const Tensor *z = G.ts + o->out;
+    if (z->flags || width(z->type) != 1 || o->p[0] != z->rank - 1) return 0;
+    Group *g = &G.groups[G.ngroups];
+    memset(g, 0, sizeof *g);
+    g->kind = 5;
+    g->first = k;
+    g->nops = 1;
+    if (!gather_operand(g, o->a, 0, users, prod, taken) || !gather_operand(g, o->b, 0, users, prod, taken) ||
+        !g->nelide)
+        return 0;
+    uint64_t w = 0;
+    for (uint32_t s = 0; s < g->nseg; s++) w += g->seg_width[s];
+    if (w != z->d[z->rank - 1]) return 0;
+    /* Plan order, for rebuilding the inner tensors. */
+    for (uint32_t a = 0; a < g->nelide; a++)
+        for (uint32_t b = a + 1; b < g->nelide; b++)
+            if (g->elide[b] < g->elide[a]) {
+                const uint32_t t = g->elide[a];
+                g->elide[a] = g->elide[b];
+                g->elide[b] = t;
+            }
+    g->in = g->seg_src[0];
+    g->out = o->out;
+    G.fuse_at[k] = (uint16_t)(G.ngroups + 1);
+    taken[k] = 1;
+    for (uint32_t e = 0; e < g->nelide; e++) {
+        G.elide[g->elide[e]] = (uint16_t)(G.ngroups + 1);
+        G.fuse_of_tensor[G.ops[g->elide[e]].out] = (uint16_t)(G.ngroups + 1);
+        taken[g->elide[e]] = 1;
+    }
+    G.ngroups++;
+    return 1;
+}
+
 static void find_groups(void)
 {
     static uint16_t users[UG_MAX_T];
     memset(G.fuse_at, 0, sizeof G.fuse_at);
     memset(G.fuse_of_tensor, 0, sizeof G.fuse_of_tensor);
+    memset(G.elide, 0, sizeof G.elide);
     G.ngroups = 0;
     count_users(users);
     const char *streams = getenv("UQ_STREAMS");
@@ -1080,6 +1196,17 @@ static void find_groups(void)
         if (!n && find_conv_add(i, users)) n = 2;
         if (!n && conv_mean && find_conv_mean(i, users)) n = 2;
         if (n) i += n - 1;
+    }
+    const char *genv = getenv("UQ_FUSE_GATHER");
+    if (!(genv && !strcmp(genv, "0"))) {
+        static uint32_t prod[UG_MAX_T];
+        static uint8_t taken[UG_MAX_OP];
+        memset(prod, 0, sizeof prod);
+        memset(taken, 0, sizeof taken);
+        for (uint32_t i = 0; i < G.h.no; i++) prod[G.ops[i].out] = i + 1;
+        for (uint32_t gi = 0; gi < G.ngroups; gi++)
+            for (uint32_t k = 0; k < G.groups[gi].nops; k++) taken[G.groups[gi].first + k] = 1;
+        for (uint32_t k = 0; k < G.h.no && G.ngroups < UG_MAX_OP / 2; k++) find_gather(k, users, prod, taken);
     }
     memset(G.fwd, 0, sizeof G.fwd);
     for (uint32_t i = 1; i < G.h.no; i++) {
@@ -1105,6 +1232,16 @@ static int materialize_group(uint32_t t)
     Group *g = &G.groups[gi - 1];
     if (!g->last_images) return 0;
     if (g->last_ext) return 22;
+    if (g->kind == 5) {
+        /* The ops the gather stood in for, from their inputs (the library's
+         * own buffers, unchanged since). */
+        int rc = 0;
+        for (uint32_t e = 0; e < g->nelide; e++) G.ptr[G.ops[g->elide[e]].out] = G.act[G.ops[g->elide[e]].out];
+        for (uint32_t e = 0; e < g->nelide && !rc; e++) rc = enqueue_op(g->elide[e], g->last_images);
+        if (!rc) rc = uqk_sync();
+        g->last_images = 0;
+        return rc ? 24 : 0;
+    }
     uint8_t *saved_in = G.ptr[g->in];
     G.ptr[g->in] = (uint8_t *)g->last_in;
     for (uint32_t k = 0; k < g->nops; k++) G.ptr[G.ops[g->first + k].out] = G.act[G.ops[g->first + k].out];
@@ -1217,11 +1354,55 @@ static int ensure_capacity(uint32_t images)
  * per-op profiling is on, and not on a caller's input buffer). Tensor
  * addresses come from G.ptr. Returns the op after the last one enqueued (a
  * group that starts before i1 runs whole). */
+/* Whether a gather (kind 5) runs fused this time: not while per-op
+ * profiling is on, and only from the library's own buffers, which still
+ * hold the same bytes if a snapshot later asks for an inner tensor. */
+static int gather_fused(const Group *g)
+{
+    if (G.profile_enabled) return 0;
+    for (uint32_t s = 0; s < g->nseg; s++)
+        if (G.ext[g->seg_src[s]]) return 0;
+    return 1;
+}
+
+static int gather_launch(Group *g, uint32_t images)
+{
+    UQKSeg segs[4];
+    const Tensor *z = G.ts + g->out;
+    uint64_t rows = images;
+    for (uint32_t d = 0; d + 1 < z->rank; d++) rows *= z->d[d];
+    for (uint32_t s = 0; s < g->nseg; s++) {
+        const Tensor *t = G.ts + g->seg_src[s];
+        segs[s].src = G.ptr[g->seg_src[s]] + g->seg_off[s];
+        segs[s].stride = t->d[t->rank - 1];
+        segs[s].width = g->seg_width[s];
+        segs[s].lut = g->seg_has_lut[s] ? G.ptr[g->seg_lut[s]] : NULL;
+        segs[s].flip = g->seg_flip[s];
+    }
+    return uqk_gather(G.ptr[g->out], z->d[z->rank - 1], segs, g->nseg, rows);
+}
+
 static int enqueue_range(uint32_t i0, uint32_t i1, uint32_t images, uint32_t *next)
 {
     uint32_t i = i0;
     for (; i < i1; i++) {
+        if (G.elide[i] && gather_fused(&G.groups[G.elide[i] - 1])) continue;
         const uint32_t g = G.fuse_at[i];
+        if (g && G.groups[g - 1].kind == 5) {
+            Group *grp = &G.groups[g - 1];
+            if (gather_fused(grp)) {
+                const int rc = gather_launch(grp, images);
+                if (rc) return rc;
+                grp->last_in = G.ptr[grp->in];
+                grp->last_images = images;
+                grp->last_ext = 0;
+                continue;
+            }
+            grp->last_images = 0;
+            const int rc = enqueue_op(i, images);
+            if (rc) return rc;
+            continue;
+        }
         /* Groups of kinds 0, 1 and 3 run fused only when the buffers they read
          * are the library's own, which still hold the same bytes if a
          * snapshot later asks for an inner tensor (materialize_group). The

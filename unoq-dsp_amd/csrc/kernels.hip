@@ -2308,6 +2308,100 @@ extern "C" int uqk_rows2(void *y, uint64_t dp, const void *a, uint64_t s1, uint6
     return 0;
 }
 
+// Row gather with tables: the fused form of a concat along the last axis
+// (code 20) of table lookups (code 22) of channel slices (code 26), such as
+// YOLO's split -> SiLU tables -> concat chains. Destination row r is the
+// concatenation of up to four segments; segment s copies `width` bytes of
+// row r of its own source (any pitch) through its own 256-entry table or
+// unchanged. Chunks of V bytes, one per thread, as k_rows2; the tables sit
+// in LDS.
+struct Gather4 {
+    int8_t *y;
+    uint64_t dp;
+    const int8_t *src[4];
+    uint64_t stride[4];
+    const uint8_t *lut[4];
+    uint32_t flip[4];
+    uint32_t c0[5];            // segment s covers chunks [c0[s], c0[s + 1]) of a row
+    uint32_t n, cpr;
+    uint64_t magic;            // ceil(2^64 / cpr), 0 when cpr == 1
+    uint64_t total;
+};
+
+template <int V>
+__global__ __launch_bounds__(256) void k_gather(Gather4 g)
+{
+    typedef typename std::conditional<V == 16, v4i, typename std::conditional<V == 4, int, int8_t>::type>::type T;
+    __shared__ uint8_t tab[4][256];
+    for (uint32_t s = 0; s < g.n; s++)
+        if (g.lut[s]) tab[s][threadIdx.x] = g.lut[s][threadIdx.x ^ g.flip[s]];
+    __syncthreads();
+    const uint64_t q = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (q >= g.total) return;
+    const uint64_t row = g.cpr == 1 ? q : __umul64hi(q, g.magic);
+    const uint32_t c = (uint32_t)(q - row * g.cpr);
+    const uint32_t s = c < g.c0[1] ? 0 : c < g.c0[2] ? 1 : c < g.c0[3] ? 2 : 3;
+    T v = *(const T *)(g.src[s] + row * g.stride[s] + (uint64_t)(c - g.c0[s]) * V);
+    if (g.lut[s]) {
+        int w[V >= 4 ? V / 4 : 1];
+        __builtin_memcpy(w, &v, sizeof(T));
+#pragma unroll
+        for (int k = 0; k < (V >= 4 ? V / 4 : 1); k++) {
+            int word = 0;
+#pragma unroll
+            for (int j = 0; j < (V >= 4 ? 4 : 1); j++) word |= (int)tab[s][(w[k] >> (8 * j)) & 0xff] << (8 * j);
+            w[k] = word;
+        }
+        __builtin_memcpy(&v, w, sizeof(T));
+    }
+    *(T *)(g.y + row * g.dp + (uint64_t)c * V) = v;
+}
+
+static uint64_t g_gather_launches;
+
+// Launches of the row gather since the library was loaded (a test hook; not
+// part of the plan ABI).
+extern "C" uint64_t uqk_gather_launches(void) { return g_gather_launches; }
+
+extern "C" int uqk_gather(void *y, uint64_t dp, const UQKSeg *segs, uint32_t n, uint64_t rows)
+{
+    if (n < 1 || n > 4) return (int)hipErrorInvalidValue;
+    uint64_t bits = (uint64_t)(uintptr_t)y | dp, width = 0;
+    for (uint32_t s = 0; s < n; s++) {
+        bits |= (uint64_t)(uintptr_t)segs[s].src | segs[s].stride | segs[s].width;
+        width += segs[s].width;
+    }
+    if (!rows || !width) return 0;
+    const int V = (bits & 15) == 0 ? 16 : (bits & 3) == 0 ? 4 : 1;
+    Gather4 g = {};
+    g.y = (int8_t *)y;
+    g.dp = dp;
+    g.n = n;
+    uint32_t at = 0;
+    for (uint32_t s = 0; s < 4; s++) {
+        g.c0[s] = at;
+        if (s < n) {
+            g.src[s] = (const int8_t *)segs[s].src;
+            g.stride[s] = segs[s].stride;
+            g.lut[s] = (const uint8_t *)segs[s].lut;
+            g.flip[s] = segs[s].flip & 0xff;
+            at += segs[s].width / V;
+        }
+    }
+    g.c0[4] = at;
+    g.cpr = at;
+    g.magic = g.cpr == 1 ? 0 : ~0ULL / g.cpr + 1;
+    g.total = rows * g.cpr;
+    if (g.total >> 32) return (int)hipErrorInvalidValue;
+    const dim3 grid((unsigned)((g.total + 255) / 256));
+    if (V == 16) UQK_LAUNCH(k_gather<16>, grid, dim3(256), 0, g_stream, g);
+    else if (V == 4) UQK_LAUNCH(k_gather<4>, grid, dim3(256), 0, g_stream, g);
+    else UQK_LAUNCH(k_gather<1>, grid, dim3(256), 0, g_stream, g);
+    UQK_LAUNCHED();
+    g_gather_launches++;
+    return 0;
+}
+
 // ---------------------------------------------------------------------------
 // Permutation (code 10, graph.c:374-390) of rank <= 4 tensors, per image:
 // out[i0,i1,i2,i3] = in[sum_d i_d * src_stride[d]], elements of 1 or 4 bytes.

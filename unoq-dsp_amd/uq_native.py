@@ -66,9 +66,10 @@ def open_library(path=None):
         fn.restype = res
         fn.argtypes = args
     # Test hooks outside the plan ABI: launches of the large-tile GEMM, of the
-    # fused bottleneck, stem, banded bottleneck and conv + mean kernels.
+    # fused bottleneck, stem, banded bottleneck, conv + mean and row gather
+    # kernels.
     for hook in ("uqk_gemm_launches", "uqk_ib_launches", "uqk_stem_conv_launches", "uqk_uib_launches",
-                 "uqk_conv_mean_launches"):
+                 "uqk_conv_mean_launches", "uqk_gather_launches"):
         getattr(lib, hook).restype = C.c_uint64
         getattr(lib, hook).argtypes = []
     # Measurement hook: the sustained int8 matrix-core rate of a register-only
