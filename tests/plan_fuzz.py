@@ -266,13 +266,24 @@ def gather_plan(seed):
     with another tensor (on either side); sometimes a half has other readers
     (its slice stays a launch), a table reads a plain tensor, the inner
     concat is of plain tensors, or an op follows. Channel counts that leave
-    rows unaligned to 4 and 16 bytes, maps of 1x1 to 9x9."""
+    rows unaligned to 4 and 16 bytes, maps of 1x1 to 9x9; every fifth plan
+    YOLO's SPPF chain of three concats."""
     rng = Rng(seed, 919191)
     p = Plan(seed)
     h, w = _pick(rng, [(1, 1), (3, 5), (8, 8), (9, 7), (2, 2)])
     x0 = p.input((1, h, w, int(_pick(rng, [8, 16, 32]))), zp=int(rng.integers(1, -128, 127)[0]))
     c = int(_pick(rng, [2, 5, 12, 16, 32, 48, 64]))
     x = p.conv(x0, c, k=1, act="none", shift=(-12, -4))
+    if seed % 5 == 4:
+        # YOLO's SPPF: three chained concats of a map and its pooled copies
+        # (nested concats, four segments); sometimes a table on the last one.
+        y1 = p.pool(x, 5, 1)
+        y2 = p.pool(y1, 5, 1)
+        y3 = p.pool(y2, 5, 1)
+        if _pick(rng, [0, 1]):
+            y3 = p.lut(y3, _random_lut(p, rng))
+        out = p.concat(p.concat(p.concat(x, y1, axis=3), y2, axis=3), y3, axis=3)
+        return p.build(p.conv(out, 16, k=1, act="none", shift=(-12, -4)))
     split = int(rng.integers(1, 1, c - 1)[0]) if c > 2 else 1
     a = p.slice(x, [0, 0, 0, 0], [1, h, w, split])
     b = p.slice(x, [0, 0, 0, split], [1, h, w, c - split])

@@ -1064,13 +1064,15 @@ static int find_stem_conv(uint32_t i, const uint16_t *users, int with_pw)
 }
 
 /* Row gathers (kind 5): a concat along the last axis (op 20) of int8/uint8
- * rows whose operands are single-use table lookups (op 22), or a single-use
- * concat along the last axis of such lookups or plain tensors; a lookup
+ * rows whose operands are single-use table lookups (op 22), or single-use
+ * concats along the last axis (nested, up to four segments) of such lookups
+ * or plain tensors; a lookup
  * whose input is a single-use slice of the last axis only (op 26) reads the
  * slice's source directly. One launch (uqk_gather) writes the concat's rows
  * from the sources through the tables, in place of the lookups, the inner
  * concat and those slices. YOLO's C3k2 blocks (split, two SiLU tables,
- * concat, concat with the bottleneck output) drop four launches each. On
+ * concat, concat with the bottleneck output) drop four launches each, its
+ * SPPF block (three chained concats of pooled maps) two. On
  * unless UQ_FUSE_GATHER=0 at load time. */
 static int rows_like(const Tensor *t, const Tensor *z)
 {
@@ -1088,12 +1090,12 @@ static int gather_operand(Group *g, uint32_t t, int depth, const uint16_t *users
     if (!rows_like(G.ts + t, z)) return 0;
     const uint32_t j = prod[t] ? prod[t] - 1 : UG_MAX_OP;
     const int inner = j < UG_MAX_OP && !taken[j] && users[t] == 1 && t != G.h.output && t != G.h.input;
-    if (inner && depth == 0 && G.ops[j].code == 20 && G.ops[j].p[0] == r - 1 && G.ops[j].a != G.ops[j].b &&
+    if (inner && depth < 3 && G.ops[j].code == 20 && G.ops[j].p[0] == r - 1 && G.ops[j].a != G.ops[j].b &&
         g->nelide < 10) {
         const uint32_t mark = g->nseg, em = g->nelide;
         g->elide[g->nelide++] = j;
-        if (gather_operand(g, G.ops[j].a, 1, users, prod, taken) &&
-            gather_operand(g, G.ops[j].b, 1, users, prod, taken))
+        if (gather_operand(g, G.ops[j].a, depth + 1, users, prod, taken) &&
+            gather_operand(g, G.ops[j].b, depth + 1, users, prod, taken))
             return 1;
         g->nseg = mark;
         g->nelide = em;
@@ -1206,7 +1208,9 @@ static void find_groups(void)
         for (uint32_t i = 0; i < G.h.no; i++) prod[G.ops[i].out] = i + 1;
         for (uint32_t gi = 0; gi < G.ngroups; gi++)
             for (uint32_t k = 0; k < G.groups[gi].nops; k++) taken[G.groups[gi].first + k] = 1;
-        for (uint32_t k = 0; k < G.h.no && G.ngroups < UG_MAX_OP / 2; k++) find_gather(k, users, prod, taken);
+        /* Last concat first, so that the outermost concat of a chain takes
+         * the inner ones. */
+        for (uint32_t k = G.h.no; k-- > 0 && G.ngroups < UG_MAX_OP / 2;) find_gather(k, users, prod, taken);
     }
     memset(G.fwd, 0, sizeof G.fwd);
     for (uint32_t i = 1; i < G.h.no; i++) {
