@@ -302,6 +302,23 @@ def gather_plan(seed):
     return p.build(out)
 
 
+def pack_plan(seed):
+    """A pack (code 19) of two to nine outputs of different sizes (tables and
+    1x1 convs of one input, rows unaligned to 4 and 16 bytes; nine is past
+    what one row gather takes)."""
+    rng = Rng(seed, 939393)
+    p = Plan(seed)
+    h, w = _pick(rng, [(1, 1), (3, 5), (8, 8), (2, 7)])
+    x = p.input((1, h, w, int(_pick(rng, [3, 8, 16]))), zp=int(rng.integers(1, -128, 127)[0]))
+    outs = []
+    for _ in range(int(_pick(rng, [2, 3, 6, 8, 9]))):
+        if _pick(rng, [0, 1]):
+            outs.append(p.lut(x, _random_lut(p, rng)))
+        else:
+            outs.append(p.conv(x, int(_pick(rng, [1, 5, 16, 20])), k=1, act="none", shift=(-12, -4)))
+    return p.build(p.pack(outs))
+
+
 def conv_mean_plan(seed):
     """A 1x1 conv followed by the global mean over its output (the classifier
     head the fused conv + mean kernel takes): maps of 1 to 64 pixels, input

@@ -13,7 +13,7 @@ import pytest
 import uq_plan as P
 import uq_workloads as W
 from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, conv_mean_plan, dw_band_plan,
-                       gather_plan,
+                       gather_plan, pack_plan,
                        dw_mfma_plan, gemm_plan, gemm_rows_plan, ib_plan, random_plan, pointwise_wide_plan,
                        rows_conv_plan, stem_conv_plan, stem_plan, uib_block)
 from test_oracle_vs_reference import (BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, softmax_table_plan,
@@ -431,6 +431,20 @@ def test_gather_fusion(lib, monkeypatch, seed):
     before = lib.uqk_gather_launches()
     _assert_same(Graph(plan, lib).run_batch(x, images), want, f"gather plan {seed} unfused")
     assert lib.uqk_gather_launches() == before
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_pack_outputs(lib, monkeypatch, seed):
+    """A pack of two to nine outputs (one row gather up to eight, a copy per
+    tensor past that or with UQ_FUSE_GATHER=0), 1-3 images, byte for byte
+    against the oracle."""
+    plan = pack_plan(seed)
+    images = 1 + seed % 3
+    x = P.random_input(plan, images, seed)
+    want = _oracle(plan, x, images)
+    _assert_same(Graph(plan, lib).run_batch(x, images), want, f"pack plan {seed}")
+    monkeypatch.setenv("UQ_FUSE_GATHER", "0")
+    _assert_same(Graph(plan, lib).run_batch(x, images), want, f"pack plan {seed}, a copy per tensor")
 
 
 @pytest.mark.parametrize("seed", range(40))

@@ -77,6 +77,7 @@ static struct {
     uint16_t fuse_at[UG_MAX_OP];
     uint16_t fuse_of_tensor[UG_MAX_T];   /* group index + 1 of an inner tensor */
     uint16_t elide[UG_MAX_OP];           /* group index + 1 of a gather (kind 5) that runs op i in its launch */
+    int pack_rows;                       /* UQ_FUSE_GATHER=0 at load: a pack (op 19) copies tensor by tensor */
     uint8_t ext[UG_MAX_T];               /* G.ptr[t] is a caller buffer this run */
     /* fwd[i]: op i's output is used only by op i + 1, a reshape (code 5) to
      * the graph output; when that output is a caller buffer, op i writes
@@ -1200,7 +1201,8 @@ static void find_groups(void)
         if (n) i += n - 1;
     }
     const char *genv = getenv("UQ_FUSE_GATHER");
-    if (!(genv && !strcmp(genv, "0"))) {
+    G.pack_rows = genv && !strcmp(genv, "0");
+    if (!G.pack_rows) {
         static uint32_t prod[UG_MAX_T];
         static uint8_t taken[UG_MAX_OP];
         memset(prod, 0, sizeof prod);
@@ -1650,6 +1652,20 @@ static int launch_op(uint32_t i, uint32_t images)
         }
         case 19: {
             const uint32_t *list = (const uint32_t *)(A + b->offset);
+            const uint32_t nl = b->bytes / 4;
+            /* Two to UQK_GATHER_MAX activations: one row gather, a row per
+             * image (UQ_FUSE_GATHER=0: a copy per tensor). */
+            UQKSeg segs[UQK_GATHER_MAX];
+            int one = nl >= 2 && nl <= UQK_GATHER_MAX && !G.pack_rows;
+            for (uint32_t j = 0; j < nl && one; j++) {
+                const Tensor *t = G.ts + list[j];
+                if (t->flags) one = 0;
+                segs[j] = (UQKSeg){G.ptr[list[j]], t->bytes, t->bytes, NULL, 0};
+            }
+            if (one) {
+                rc = uqk_gather(zp, z->bytes, segs, nl, images);
+                break;
+            }
             size_t off = 0;
             for (uint32_t j = 0; j < b->bytes / 4 && !rc; j++) {
                 const Tensor *t = G.ts + list[j];

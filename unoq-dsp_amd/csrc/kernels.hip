@@ -2310,29 +2310,29 @@ extern "C" int uqk_rows2(void *y, uint64_t dp, const void *a, uint64_t s1, uint6
 
 // Row gather with tables: the fused form of a concat along the last axis
 // (code 20) of table lookups (code 22) of channel slices (code 26), such as
-// YOLO's split -> SiLU tables -> concat chains. Destination row r is the
-// concatenation of up to four segments; segment s copies `width` bytes of
-// row r of its own source (any pitch) through its own 256-entry table or
-// unchanged. Chunks of V bytes, one per thread, as k_rows2; the tables sit
-// in LDS.
-struct Gather4 {
+// YOLO's split -> SiLU tables -> concat chains, and of a pack of several
+// outputs (code 19). Destination row r is the concatenation of up to
+// UQK_GATHER_MAX segments; segment s copies `width` bytes of row r of its own
+// source (any pitch) through its own 256-entry table or unchanged. Chunks of
+// V bytes, one per thread, as k_rows2; the tables sit in LDS.
+struct Gather {
     int8_t *y;
     uint64_t dp;
-    const int8_t *src[4];
-    uint64_t stride[4];
-    const uint8_t *lut[4];
-    uint32_t flip[4];
-    uint32_t c0[5];            // segment s covers chunks [c0[s], c0[s + 1]) of a row
+    const int8_t *src[UQK_GATHER_MAX];
+    uint64_t stride[UQK_GATHER_MAX];
+    const uint8_t *lut[UQK_GATHER_MAX];
+    uint32_t flip[UQK_GATHER_MAX];
+    uint32_t c0[UQK_GATHER_MAX + 1];   // segment s covers chunks [c0[s], c0[s + 1]) of a row
     uint32_t n, cpr;
     uint64_t magic;            // ceil(2^64 / cpr), 0 when cpr == 1
     uint64_t total;
 };
 
 template <int V>
-__global__ __launch_bounds__(256) void k_gather(Gather4 g)
+__global__ __launch_bounds__(256) void k_gather(Gather g)
 {
     typedef typename std::conditional<V == 16, v4i, typename std::conditional<V == 4, int, int8_t>::type>::type T;
-    __shared__ uint8_t tab[4][256];
+    __shared__ uint8_t tab[UQK_GATHER_MAX][256];
     for (uint32_t s = 0; s < g.n; s++)
         if (g.lut[s]) tab[s][threadIdx.x] = g.lut[s][threadIdx.x ^ g.flip[s]];
     __syncthreads();
@@ -2340,7 +2340,8 @@ __global__ __launch_bounds__(256) void k_gather(Gather4 g)
     if (q >= g.total) return;
     const uint64_t row = g.cpr == 1 ? q : __umul64hi(q, g.magic);
     const uint32_t c = (uint32_t)(q - row * g.cpr);
-    const uint32_t s = c < g.c0[1] ? 0 : c < g.c0[2] ? 1 : c < g.c0[3] ? 2 : 3;
+    uint32_t s = 0;
+    while (s + 1 < g.n && c >= g.c0[s + 1]) s++;
     T v = *(const T *)(g.src[s] + row * g.stride[s] + (uint64_t)(c - g.c0[s]) * V);
     if (g.lut[s]) {
         int w[V >= 4 ? V / 4 : 1];
@@ -2365,7 +2366,7 @@ extern "C" uint64_t uqk_gather_launches(void) { return g_gather_launches; }
 
 extern "C" int uqk_gather(void *y, uint64_t dp, const UQKSeg *segs, uint32_t n, uint64_t rows)
 {
-    if (n < 1 || n > 4) return (int)hipErrorInvalidValue;
+    if (n < 1 || n > UQK_GATHER_MAX) return (int)hipErrorInvalidValue;
     uint64_t bits = (uint64_t)(uintptr_t)y | dp, width = 0;
     for (uint32_t s = 0; s < n; s++) {
         bits |= (uint64_t)(uintptr_t)segs[s].src | segs[s].stride | segs[s].width;
@@ -2373,12 +2374,12 @@ extern "C" int uqk_gather(void *y, uint64_t dp, const UQKSeg *segs, uint32_t n, 
     }
     if (!rows || !width) return 0;
     const int V = (bits & 15) == 0 ? 16 : (bits & 3) == 0 ? 4 : 1;
-    Gather4 g = {};
+    Gather g = {};
     g.y = (int8_t *)y;
     g.dp = dp;
     g.n = n;
     uint32_t at = 0;
-    for (uint32_t s = 0; s < 4; s++) {
+    for (uint32_t s = 0; s < UQK_GATHER_MAX; s++) {
         g.c0[s] = at;
         if (s < n) {
             g.src[s] = (const int8_t *)segs[s].src;
@@ -2388,7 +2389,7 @@ extern "C" int uqk_gather(void *y, uint64_t dp, const UQKSeg *segs, uint32_t n, 
             at += segs[s].width / V;
         }
     }
-    g.c0[4] = at;
+    g.c0[UQK_GATHER_MAX] = at;
     g.cpr = at;
     g.magic = g.cpr == 1 ? 0 : ~0ULL / g.cpr + 1;
     g.total = rows * g.cpr;

@@ -151,9 +151,10 @@ int uqk_d2d_2d(void *dst, size_t dpitch, const void *src, size_t spitch, size_t 
  * (w2 bytes, pitch s2; w2 may be 0). One kernel launch. */
 int uqk_rows2(void *y, uint64_t dp, const void *a, uint64_t s1, uint64_t w1, const void *b, uint64_t s2, uint64_t w2,
               uint64_t rows);
-/* Rows of up to four segments, each `width` bytes per row from its own
+/* Rows of up to UQK_GATHER_MAX segments, each `width` bytes per row from its own
  * source (row pitch `stride`), mapped through a 256-entry table (index byte
  * ^ flip) when `lut` is set: y row r = seg 0 | seg 1 | ... (pitch dp). */
+#define UQK_GATHER_MAX 8
 typedef struct {
     const void *src;
     uint64_t stride;
