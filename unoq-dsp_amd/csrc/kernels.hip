@@ -1863,14 +1863,25 @@ static size_t dw_mfma_plan(const UQKSpatial *d, DwMArgs *t, uint32_t batches)
     if (d->dw_rows > 0) {
         if (band > d->dw_rows) band = d->dw_rows;
     } else if (batches && blocks_of(band, (d->oh + band - 1) / band) < DWM_BLOCKS) {
+        // 5x5 layers (25 taps per staged byte) take up to twice the blocks,
+        // and of the band counts passed on the way the last that divides
+        // the map exactly wins over a later uneven one: 64 x 56x56x96 5x5
+        // s2 (28 output rows) 11.0-11.2 us in bands of 10 (3 bands, the old
+        // rule), 9.3 in bands of 6 (5, uneven), 8.7-8.8 in bands of 7 (4);
+        // 3x3 layers keep 1,024 blocks (112x112x32 3x3 s1: 18.0 us in bands
+        // of 14, 18.6-18.9 in bands of 8 or 7).
+        const long target = ks == 5 ? 2 * DWM_BLOCKS : DWM_BLOCKS;
         int nb = (d->oh + band - 1) / band;
         band = (d->oh + nb - 1) / nb;
-        while (band > 1 && blocks_of(band, nb) < DWM_BLOCKS) {
+        int pick = band;
+        while (band > 1 && blocks_of(band, nb) < target) {
             const int nb2 = nb + 1, band2 = (d->oh + nb2 - 1) / nb2;
             if (((band2 - 1) * s + ks) * 4 > band2 * s * 5) break;
             nb = nb2;
             band = band2;
+            if (d->oh % band == 0 || d->oh % pick != 0) pick = band;
         }
+        band = pick;
     }
     t->band = band;
     t->bands = (d->oh + band - 1) / band;
