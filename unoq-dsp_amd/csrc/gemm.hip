@@ -737,6 +737,12 @@ extern "C" int uqk_gemm_take(const UQKSpatial *d, uint64_t pixels)
 {
     if (d->gemm == 0 || !uqk_gemm_ok(d) || pixels >= 0x7fffffffULL) return 0;
     if (d->gemm == 1) return 1;
+    // Also deep convs the general kernel would run on per-lane gathers (no
+    // row staging within its LDS): a 3x3 stride-2 128 -> 128 conv at 40x40,
+    // 64 images (K = 1,152, 25,600 pixels), 31.0 -> 16.3 us; smaller or
+    // shallower ones (6,400 x 256 or 25,600 x 64 at K = 1,152, K = 576)
+    // measured slower here.
+    if (d->mode == UQK_G16 && d->K >= 1024 && pixels * (uint64_t)d->oc >= (1ULL << 21)) return 1;
     return d->K >= 512 && pixels * (uint64_t)d->oc >= (1ULL << 24);
 }
 
