@@ -302,6 +302,27 @@ def gather_plan(seed):
     return p.build(out)
 
 
+def conv_lut_plan(seed):
+    """A conv (1x1, 3x3, stride 1 or 2, with or without its own post table)
+    whose output feeds only a table lookup, sometimes followed by another op;
+    sometimes the conv's output has a second reader (then nothing is fused)."""
+    rng = Rng(seed, 959595)
+    p = Plan(seed)
+    h, w = _pick(rng, [(1, 1), (5, 7), (16, 16), (9, 3)])
+    x = p.input((1, h, w, int(_pick(rng, [3, 8, 16, 32, 64]))), zp=int(rng.integers(1, -128, 127)[0]))
+    k = int(_pick(rng, [1, 1, 3]))
+    y = p.conv(x, int(_pick(rng, [8, 16, 20, 64, 80])), k=k, stride=int(_pick(rng, [1, 2])) if k == 3 else 1,
+               act=_pick(rng, ["none", "relu", "relu6"]), q6=int(rng.integers(1, 1, 200)[0]),
+               lut=_random_lut(p, rng) if _pick(rng, [0, 1]) else None, shift=(-12, -4),
+               w_sigma=_pick(rng, [3, 40, 90]))
+    z = p.lut(y, _random_lut(p, rng))
+    if _pick(rng, [0, 0, 0, 1]):
+        z = p.concat(z, y, axis=3)
+    if _pick(rng, [0, 1]):
+        z = p.conv(z, 16, k=1, act="none", shift=(-12, -4))
+    return p.build(z)
+
+
 def pack_plan(seed):
     """A pack (code 19) of two to nine outputs of different sizes (tables and
     1x1 convs of one input, rows unaligned to 4 and 16 bytes; nine is past

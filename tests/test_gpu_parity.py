@@ -13,7 +13,7 @@ import pytest
 import uq_plan as P
 import uq_workloads as W
 from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, conv_mean_plan, dw_band_plan,
-                       gather_plan, pack_plan,
+                       gather_plan, pack_plan, conv_lut_plan,
                        dw_mfma_plan, gemm_plan, gemm_rows_plan, ib_plan, random_plan, pointwise_wide_plan,
                        rows_conv_plan, stem_conv_plan, stem_plan, uib_block)
 from test_oracle_vs_reference import (BMM_SHAPES, TRANSPOSES, bmm_plan, softmax_plan, softmax_table_plan,
@@ -431,6 +431,26 @@ def test_gather_fusion(lib, monkeypatch, seed):
     before = lib.uqk_gather_launches()
     _assert_same(Graph(plan, lib).run_batch(x, images), want, f"gather plan {seed} unfused")
     assert lib.uqk_gather_launches() == before
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_conv_lut_fusion(lib, monkeypatch, seed):
+    """A conv whose output only feeds a table lookup runs as one conv launch
+    with the tables composed: 1-3 images against the oracle, a snapshot of
+    the conv's output rebuilt after a host run, and the same plans unfused
+    (UQ_FUSE_LUT=0)."""
+    plan = conv_lut_plan(seed)
+    images = 1 + seed % 3
+    x = P.random_input(plan, images, seed)
+    want = _oracle(plan, x, images)
+    g = Graph(plan, lib)
+    _assert_same(g.run_batch(x, images), want, f"conv+lut plan {seed}")
+    conv_out = P.op_records(plan)[0][3]
+    nbytes = images * P.tensor_records(plan)[conv_out][1]
+    _, snap = oracle_run(plan, x, images, P.output_bytes(plan), snap=conv_out, snap_bytes=nbytes)
+    _assert_same(g.snapshot_images(conv_out, nbytes), snap, f"conv+lut plan {seed}: conv output snapshot")
+    monkeypatch.setenv("UQ_FUSE_LUT", "0")
+    _assert_same(Graph(plan, lib).run_batch(x, images), want, f"conv+lut plan {seed} unfused")
 
 
 @pytest.mark.parametrize("seed", range(20))

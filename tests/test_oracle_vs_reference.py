@@ -28,7 +28,7 @@ import pytest
 import uq_plan as P
 import uq_workloads as W
 from plan_fuzz import (ATTENTION_OPS, CONSTANT_OPS, conv_add_bytes_plan, conv_add_plan, conv_mean_plan, dw_band_plan,
-                       gather_plan,
+                       gather_plan, conv_lut_plan,
                        dw_mfma_plan, gemm_plan, gemm_rows_plan, ib_plan, random_plan, pointwise_wide_plan,
                        rows_conv_plan, stem_conv_plan, stem_plan, uib_plan)
 from refs import oracle_run, ref_plain, ref_release
@@ -128,7 +128,7 @@ def test_constant_operand_plans_match_reference(seed):
 
 @pytest.mark.parametrize("maker", [dw_mfma_plan, stem_plan, rows_conv_plan, pointwise_wide_plan, gemm_plan,
                                    gemm_rows_plan, dw_band_plan, ib_plan, stem_conv_plan, uib_plan, conv_mean_plan,
-                                   gather_plan])
+                                   gather_plan, conv_lut_plan])
 @pytest.mark.parametrize("seed", range(12))
 def test_kernel_shape_fuzz_matches_reference(maker, seed):
     """Shapes aimed at the GPU's specialised kernels (matrix-core depthwise,

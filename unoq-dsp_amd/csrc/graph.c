@@ -35,15 +35,17 @@ typedef struct { uint32_t code, a, b, out, p[4]; } Op;
  * (kind 0), a conv whose residual add runs in its epilogue (kind 1), a stem
  * conv, the 3x3 stride-2 conv over its output and optionally the 1x1 after
  * that (kind 2), a banded universal inverted bottleneck (kind 3), a 1x1
- * conv and the mean over its whole output (kind 4), or a concat whose
+ * conv and the mean over its whole output (kind 4), a concat whose
  * operands' table lookups, inner concats and slices run inside its launch
- * (kind 5, find_gather). */
+ * (kind 5, find_gather), or a conv whose output only feeds a table lookup,
+ * run with the two tables composed (kind 6, find_conv_lut). */
 typedef struct {
     int kind;
     UQKIb desc;
     UQKUib ub;                       /* kind 3 */
     UQKAdd add;                      /* kind 1; add.res is set per launch */
     UQKMean mean;                    /* kind 4 */
+    UQKSpatial sp;                   /* kind 6: the conv with the composed post table */
     /* kind 5: segments of the output rows (source tensor, byte offset in its
      * rows, bytes per row, table tensor or none, index flip) and the earlier
      * ops the launch stands in for, in plan order */
@@ -536,7 +538,7 @@ static int choose_nt(int oc, uint64_t rows_per_image)
     return best;
 }
 
-typedef struct { size_t w, epi, kmap, end; } Layout;
+typedef struct { size_t w, epi, kmap, post, end; } Layout;
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -608,14 +610,15 @@ static ConvPlan conv_plan(const Op *o)
 static Layout spatial_layout(const Op *o, size_t at)
 {
     const int32_t *q = (const int32_t *)(G.arena + G.ts[o->p[0]].offset);
-    Layout L = {at, at, at, at};
+    Layout L = {at, at, at, at, at};
     int oc = q[17];
     if (o->code == 14) {
         ConvPlan c = conv_plan(o);
         L.w = at;
         L.epi = align256(L.w + (size_t)c.oc_pad * c.kpad);
         L.kmap = align256(L.epi + (size_t)oc * 32);
-        L.end = align256(L.kmap + (size_t)c.table_bytes);
+        L.post = align256(L.kmap + (size_t)c.table_bytes);   /* a composed post table (kind 6) */
+        L.end = L.post + 256;
     } else if (o->code == 15) {
         /* Tap words: (taps + 3) / 4 groups for k_dw_tile, kh * 2 rows of one
          * or two words for k_dw_win; room for either. */
@@ -861,6 +864,45 @@ static int find_conv_add(uint32_t i, const uint16_t *users)
 /* A 1x1 conv whose output, used by nothing else, is averaged over the whole
  * map by the next op (MobileNet's classifier head) and that fits head.hip.
  * On unless UQ_FUSE_MEAN=0 at load time. */
+/* A conv (op 14) whose output, used by nothing else and not the plan's,
+ * feeds only the next op, a byte table lookup (op 22): the lookup's table
+ * composed with the conv's own post table (or with the identity) becomes the
+ * post table of one conv launch (the composition sits in the 256 bytes the
+ * conv's device tables reserve for it). YOLO's detection heads. On unless
+ * UQ_FUSE_LUT=0 at load time. */
+static int find_conv_lut(uint32_t i, const uint16_t *users, uint8_t *pool, const Layout *layouts)
+{
+    const Op *c = G.ops + i, *l = G.ops + i + 1;
+    if (c->code != 14 || l->code != 22 || l->a != c->out) return 0;
+    const uint32_t t = c->out;
+    if (users[t] != 1 || t == G.h.output || G.ts[t].flags || !G.ts[l->b].flags || G.ts[l->b].bytes < 256 ||
+        width(G.ts[t].type) != 1)
+        return 0;
+    const uint8_t *table = G.arena + G.ts[l->b].offset;
+    const uint8_t *own = c->p[1] ? G.arena + G.ts[c->p[1] - 1].offset : NULL;
+    const uint32_t flip = G.ts[t].type == 3 ? 128u : 0u;
+    uint8_t *post = pool + layouts[i].post;
+    /* Index v + 128 of the conv's requantised value v: its output byte is
+     * the own table's entry there, else the two's-complement byte of v. */
+    for (uint32_t v = 0; v < 256; v++) {
+        const uint32_t byte = own ? own[v] : (uint32_t)(uint8_t)(v - 128u);
+        post[v] = table[byte ^ flip];
+    }
+    Group *g = &G.groups[G.ngroups];
+    memset(g, 0, sizeof *g);
+    g->kind = 6;
+    g->sp = G.sp[i];
+    g->sp.lut = G.dev_prep + layouts[i].post;
+    g->first = i;
+    g->nops = 2;
+    g->in = c->a;
+    g->out = l->out;
+    G.fuse_at[i] = (uint16_t)(G.ngroups + 1);
+    G.fuse_of_tensor[t] = (uint16_t)(G.ngroups + 1);
+    G.ngroups++;
+    return 1;
+}
+
 static int find_conv_mean(uint32_t i, const uint16_t *users)
 {
     const Op *c = G.ops + i, *mn = G.ops + i + 1;
@@ -1173,7 +1215,7 @@ static int find_gather(uint32_t k, const uint16_t *users, const uint32_t *prod, 
     return 1;
 }
 
-static void find_groups(void)
+static void find_groups(uint8_t *pool, const Layout *layouts)
 {
     static uint16_t users[UG_MAX_T];
     memset(G.fuse_at, 0, sizeof G.fuse_at);
@@ -1190,6 +1232,8 @@ static void find_groups(void)
     const int stem = !(senv && !strcmp(senv, "0")), stem_pw = !(senv && !strcmp(senv, "2"));
     const char *menv = getenv("UQ_FUSE_MEAN");
     const int conv_mean = !(menv && !strcmp(menv, "0"));
+    const char *lenv = getenv("UQ_FUSE_LUT");
+    const int conv_lut = !(lenv && !strcmp(lenv, "0"));
     const char *uenv = getenv("UQ_FUSE_UIB");
     const int uib = !uenv ? 1 : !strcmp(uenv, "0") ? 0 : !strcmp(uenv, "2") ? 2 : 1;
     for (uint32_t i = 0; i + 1 < G.h.no; i++) {
@@ -1198,6 +1242,7 @@ static void find_groups(void)
         if (!n && bottleneck) n = find_bottleneck(i, users);
         if (!n && find_conv_add(i, users)) n = 2;
         if (!n && conv_mean && find_conv_mean(i, users)) n = 2;
+        if (!n && conv_lut && find_conv_lut(i, users, pool, layouts)) n = 2;
         if (n) i += n - 1;
     }
     const char *genv = getenv("UQ_FUSE_GATHER");
@@ -1281,7 +1326,7 @@ static int prepare_device(void)
         const Op *o = G.ops + i;
         if (o->code == 14 || o->code == 15 || o->code == 16) prepare_spatial(i, layouts + i, host_pool);
     }
-    find_groups();
+    find_groups(host_pool, layouts);
     int rc = uqk_h2d(G.dev_arena, G.arena, G.h.arena_bytes);
     if (!rc) rc = uqk_h2d(G.dev_prep, host_pool, at + 256);
     if (!rc) rc = uqk_sync();
@@ -1424,6 +1469,8 @@ static int enqueue_range(uint32_t i0, uint32_t i1, uint32_t images, uint32_t *ne
                 rc = uqk_ib(&grp->desc, G.ptr[grp->in], G.ptr[grp->out], images);
             } else if (grp->kind == 3) {
                 rc = uqk_uib(&grp->ub, G.ptr[grp->in], G.ptr[grp->out], images);
+            } else if (grp->kind == 6) {
+                rc = uqk_conv(&grp->sp, G.ptr[grp->in], G.ptr[grp->out], images * G.ts[G.ops[i].a].d[0]);
             } else if (grp->kind == 4) {
                 rc = uqk_conv_mean(G.sp + i, &grp->mean, G.ptr[grp->in], G.ptr[grp->out],
                                    images * G.ts[G.ops[i].a].d[0]);
